@@ -1,0 +1,97 @@
+"""Build libjanus_hip.so (gfx950) and the CPU oracle in-tree.
+
+The library is compiled with hipcc for gfx950 only, one object per source
+file in parallel, then linked as a shared object next to this package so the
+GPU box loads it straight from the repository tree.
+
+Usage: python -m janus_amd.build [--jobs N] [--no-oracle]
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libjanus_hip.so"
+ORACLE_DIR = ROOT / "oracle"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    "-munsafe-fp-atomics",
+    # Packed FP32 instructions stay off (toolchain notes).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build_library(jobs: int | None = None, verbose: bool = True) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libjanus_hip.so."""
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    BUILD.mkdir(exist_ok=True)
+    srcs = _sources()
+    jobs = jobs or min(8, len(srcs), os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"[janus_amd.build] built {LIB.relative_to(ROOT)} from {len(srcs)} sources", flush=True)
+    return LIB
+
+
+def build_oracle(verbose: bool = True) -> Path:
+    """Compile the CPU oracle (test infrastructure) with its Makefile."""
+    res = subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), "-B", "liboracle.so"],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{res.stdout}\n{res.stderr}")
+    if verbose:
+        print("[janus_amd.build] built oracle/liboracle.so", flush=True)
+    return ORACLE_DIR / "liboracle.so"
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--no-oracle", action="store_true")
+    args = ap.parse_args(argv)
+    build_library(args.jobs)
+    if not args.no_oracle:
+        build_oracle()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,579 @@
+// gemv.hip -- dequant-fused matrix-vector products for gfx950 (wave64).
+//
+// Replaces gemm_q8_0_into / gemm_q4_k_into / matmul::gemm at M=1
+// (crates/janus-engine/src/compute/ops/quantized.rs:188-378,
+// ops/matmul.rs:228-298; shaders gemm_q8_0.wgsl, gemm_q4_k.wgsl, gemm.wgsl)
+// and adds Q4_0, which the reference cannot run (compute/engine.rs:833-838).
+//
+// Design (one launch per product, HBM-bound):
+//  * The activation vector x is staged once per workgroup into LDS, padded
+//    per 32-element block (no bank conflicts on 16-byte LDS reads), together
+//    with its 16-element partial sums (used by the Q4_K mins and the Q4_0 /
+//    Q8_0 offset terms).
+//  * LPR lanes cooperate on a row; each lane owns the row's units
+//    u = lane, lane + LPR, ... and reads each unit's quants with one or two
+//    128-bit loads, so a wavefront's load covers LPR*16 contiguous bytes.
+//  * A wavefront processes R rows at once: x registers loaded from LDS are
+//    reused for all R rows, and all R*units weight loads are issued before
+//    any arithmetic so the wave keeps many KB in flight.
+//  * Nibbles are unpacked in registers: f32 activations use
+//    v_cvt_f32_ubyte{0..3} + FMA; f16 activations build binary16 pairs with
+//    the 0x6400 exponent trick and reduce with v_dot2_f32_f16 (exact
+//    products, fp32 accumulation).
+//  * The R partial sums are reduced across the LPR lanes with a transposed
+//    butterfly (log2 R exchange steps that halve the live values, then a
+//    plain xor butterfly), so the reduction costs O(R + log LPR) shuffles.
+#include "internal.h"
+
+namespace {
+
+constexpr int XB = 32;                 // activation elements per LDS block
+template <typename XT> struct XLayout;
+template <> struct XLayout<float> {    // 32 floats + 4 pad = 144 B
+    static constexpr int STRIDE = 36;
+};
+template <> struct XLayout<_Float16> { // 32 halves + 8 pad = 80 B
+    static constexpr int STRIDE = 40;
+};
+
+__device__ __forceinline__ float cvt_b0(uint32_t u) { return (float)(u & 0xffu); }
+__device__ __forceinline__ float cvt_b1(uint32_t u) { return (float)((u >> 8) & 0xffu); }
+__device__ __forceinline__ float cvt_b2(uint32_t u) { return (float)((u >> 16) & 0xffu); }
+__device__ __forceinline__ float cvt_b3(uint32_t u) { return (float)(u >> 24); }
+
+__device__ __forceinline__ jh2 as_h2(uint32_t u) { return __builtin_bit_cast(jh2, u); }
+__device__ __forceinline__ float dot2(jh2 a, jh2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// ---------------------------------------------------------------------------
+// x staging
+// ---------------------------------------------------------------------------
+// Writes x[0..k) into LDS: element e goes to block e/32, slot e%32. For f16
+// with PERM, each group of four (a,b,c,d) is stored as (a,c,b,d) so a u32 of
+// packed nibbles maps onto (x[i], x[i+2]) pairs. sx16[g] = sum of x[16g..16g+16).
+template <typename XIN, typename XT, bool PERM>
+__device__ void stage_x(const XIN *__restrict__ x, uint32_t k, XT *xs, float *sx16) {
+    const int groups = (int)((k + 15) / 16);
+    for (int g = threadIdx.x; g < groups; g += blockDim.x) {
+        float v[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            uint32_t e = (uint32_t)g * 16 + t;
+            v[t] = e < k ? (float)x[e] : 0.0f;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) s += v[t];
+        sx16[g] = s;
+        int blk = g >> 1, off = (g & 1) * 16;
+        XT *dst = xs + blk * XLayout<XT>::STRIDE + off;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (PERM) {
+                dst[4 * q + 0] = (XT)v[4 * q + 0];
+                dst[4 * q + 1] = (XT)v[4 * q + 2];
+                dst[4 * q + 2] = (XT)v[4 * q + 1];
+                dst[4 * q + 3] = (XT)v[4 * q + 3];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) dst[4 * q + t] = (XT)v[4 * q + t];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// formats. Each provides: UNIT (weights per lane-unit), a weight register
+// record W with load(), an x register record per activation type with
+// loadx(), and dot(W, X) returning the unit's contribution in fp32.
+// ---------------------------------------------------------------------------
+
+struct WPtr {
+    const uint8_t *qs;
+    const uint16_t *sc;
+};
+
+// ---- Q4_0: 16 B nibbles (GGML order) + binary16 scale per 32 weights -------
+struct FQ4_0 {
+    static constexpr int UNIT = 32;
+    static constexpr bool PERM = true;
+    struct W { uint4 q; uint16_t d; };
+    __device__ static W load(WPtr w, size_t unit) {
+        W r;
+        r.q = ld_stream((const uint4 *)w.qs + unit);
+        r.d = w.sc[unit];
+        return r;
+    }
+    struct XF { jf4 v[8]; float s; };          // x[0..32) and sum(x)
+    __device__ static XF loadx(const float *xs, const float *sx16, int u) {
+        XF r;
+        const jf4 *p = (const jf4 *)(xs + u * XLayout<float>::STRIDE);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+        r.s = sx16[2 * u] + sx16[2 * u + 1];
+        return r;
+    }
+    __device__ static float dot(const W &w, const XF &x) {
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            jf4 xl = x.v[i], xh = x.v[4 + i];   // elements 4i..4i+3 and 16+4i..
+            s0 = fmaf(cvt_b0(lo), xl.x, s0);
+            s1 = fmaf(cvt_b1(lo), xl.y, s1);
+            s0 = fmaf(cvt_b2(lo), xl.z, s0);
+            s1 = fmaf(cvt_b3(lo), xl.w, s1);
+            s0 = fmaf(cvt_b0(hi), xh.x, s0);
+            s1 = fmaf(cvt_b1(hi), xh.y, s1);
+            s0 = fmaf(cvt_b2(hi), xh.z, s0);
+            s1 = fmaf(cvt_b3(hi), xh.w, s1);
+        }
+        // sum (q-8) x = sum q x - 8 sum x
+        return h2f(w.d) * fmaf(-8.0f, x.s, s0 + s1);
+    }
+    struct XH { jh2 v[16]; };
+    __device__ static XH loadx(const _Float16 *xs, const float *, int u) {
+        XH r;
+        const uint4 *p = (const uint4 *)(xs + u * XLayout<_Float16>::STRIDE);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint4 t = p[i];
+            r.v[4 * i + 0] = as_h2(t.x);
+            r.v[4 * i + 1] = as_h2(t.y);
+            r.v[4 * i + 2] = as_h2(t.z);
+            r.v[4 * i + 3] = as_h2(t.w);
+        }
+        return r;
+    }
+    __device__ static float dot(const W &w, const XH &x) {
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        const jh2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t u = q[i];
+            // low nibbles: elements 4i..4i+3; high nibbles: 16+4i..16+4i+3.
+            jh2 a = as_h2((u & 0x000f000fu) | 0x64006400u) - off;          // (4i, 4i+2)
+            jh2 c = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - off;   // (4i+1, 4i+3)
+            jh2 b = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - off;   // (16+4i, 16+4i+2)
+            jh2 e = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - off;  // (16+4i+1, ..+3)
+            // x pairs (permuted staging): v[2g] = (x[4g], x[4g+2]), v[2g+1] = (x[4g+1], x[4g+3])
+            s0 = dot2(a, x.v[2 * i], s0);
+            s1 = dot2(c, x.v[2 * i + 1], s1);
+            s0 = dot2(b, x.v[8 + 2 * i], s0);
+            s1 = dot2(e, x.v[8 + 2 * i + 1], s1);
+        }
+        return h2f(w.d) * (s0 + s1);
+    }
+};
+
+// ---- Q8_0: 32 B int8 + binary16 scale (exp 31 -> 1e38) per 32 weights ------
+struct FQ8_0 {
+    static constexpr int UNIT = 32;
+    static constexpr bool PERM = true;
+    struct W { uint4 q0, q1; uint16_t d; };
+    __device__ static W load(WPtr w, size_t unit) {
+        W r;
+        const uint4 *p = (const uint4 *)w.qs + 2 * unit;
+        r.q0 = ld_stream(p);
+        r.q1 = ld_stream(p + 1);
+        r.d = w.sc[unit];
+        return r;
+    }
+    using XF = FQ4_0::XF;
+    using XH = FQ4_0::XH;
+    __device__ static XF loadx(const float *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
+    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
+    __device__ static float dot(const W &w, const XF &x) {
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t u = q[i] ^ 0x80808080u;   // int8 q -> unsigned q + 128
+            jf4 xv = x.v[i];
+            s0 = fmaf(cvt_b0(u), xv.x, s0);
+            s1 = fmaf(cvt_b1(u), xv.y, s1);
+            s0 = fmaf(cvt_b2(u), xv.z, s0);
+            s1 = fmaf(cvt_b3(u), xv.w, s1);
+        }
+        return h2f_q8(w.d) * fmaf(-128.0f, x.s, s0 + s1);
+    }
+    __device__ static float dot(const W &w, const XH &x) {
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const jh2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t u = q[i] ^ 0x80808080u;
+            jh2 a = as_h2((u & 0x00ff00ffu) | 0x64006400u) - off;         // (4i, 4i+2)
+            jh2 c = as_h2(((u >> 8) & 0x00ff00ffu) | 0x64006400u) - off;  // (4i+1, 4i+3)
+            s0 = dot2(a, x.v[2 * i], s0);
+            s1 = dot2(c, x.v[2 * i + 1], s1);
+        }
+        return h2f_q8(w.d) * (s0 + s1);
+    }
+};
+
+// ---- Q4_K: GGML 144-byte super-blocks; a unit is one 16-byte quant chunk ----
+// Chunk c (0..7) of a super-block covers qs bytes 16c..16c+15, i.e. j = c/2,
+// h = c%2: low nibbles -> elements 64j+16h+t (sub-block 2j), high nibbles ->
+// 64j+32+16h+t (sub-block 2j+1), t = 0..15. Weight = (d*sc)*q - dmin*m
+// (shaders/gemm_q4_k.wgsl:82-113).
+struct FQ4_K {
+    static constexpr int UNIT = 32;
+    static constexpr bool PERM = true;
+    struct W { uint4 q; uint4 hdr; };
+    __device__ static W load(WPtr w, size_t unit) {
+        size_t sb = unit >> 3;
+        int c = (int)(unit & 7);
+        const uint4 *blk = (const uint4 *)(w.qs + sb * 144);
+        W r;
+        r.hdr = blk[0];
+        r.q = ld_stream(blk + 1 + c);
+        return r;
+    }
+    // x for one chunk: 16 low-nibble elements and 16 high-nibble elements.
+    struct XF { jf4 lo[4], hi[4]; float slo, shi; int c; };
+    __device__ static XF loadx(const float *xs, const float *sx16, int u) {
+        int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
+        int blo = sb * 8 + 2 * j, bhi = blo + 1;   // 32-element LDS blocks
+        XF r;
+        const jf4 *pl = (const jf4 *)(xs + blo * XLayout<float>::STRIDE + 16 * h);
+        const jf4 *ph = (const jf4 *)(xs + bhi * XLayout<float>::STRIDE + 16 * h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { r.lo[i] = pl[i]; r.hi[i] = ph[i]; }
+        r.slo = sx16[2 * blo + h];
+        r.shi = sx16[2 * bhi + h];
+        r.c = c;
+        return r;
+    }
+    struct XH { jh2 lo[8], hi[8]; float slo, shi; int c; };
+    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) {
+        int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
+        int blo = sb * 8 + 2 * j, bhi = blo + 1;
+        XH r;
+        const uint4 *pl = (const uint4 *)(xs + blo * XLayout<_Float16>::STRIDE + 16 * h);
+        const uint4 *ph = (const uint4 *)(xs + bhi * XLayout<_Float16>::STRIDE + 16 * h);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint4 a = pl[i], b = ph[i];
+            r.lo[4 * i + 0] = as_h2(a.x); r.lo[4 * i + 1] = as_h2(a.y);
+            r.lo[4 * i + 2] = as_h2(a.z); r.lo[4 * i + 3] = as_h2(a.w);
+            r.hi[4 * i + 0] = as_h2(b.x); r.hi[4 * i + 1] = as_h2(b.y);
+            r.hi[4 * i + 2] = as_h2(b.z); r.hi[4 * i + 3] = as_h2(b.w);
+        }
+        r.slo = sx16[2 * blo + h];
+        r.shi = sx16[2 * bhi + h];
+        r.c = c;
+        return r;
+    }
+    // (sc, m) pair of sub-block `sub` from the 12 scale bytes held in hdr.y..w.
+    __device__ static void scale_min(const uint4 &hdr, int sub, float &sc, float &mn) {
+        uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;   // bytes 0-3, 4-7, 8-11
+        uint32_t scv, mnv;
+        if (sub < 4) {
+            scv = (s0 >> (8 * sub)) & 63u;
+            mnv = (s1 >> (8 * sub)) & 63u;
+        } else {
+            int i = sub - 4;
+            uint32_t b8 = (s2 >> (8 * i)) & 0xffu;
+            scv = (b8 & 15u) | (((s0 >> (8 * i)) & 0xffu) >> 6 << 4);
+            mnv = (b8 >> 4) | (((s1 >> (8 * i)) & 0xffu) >> 6 << 4);
+        }
+        sc = (float)scv;
+        mn = (float)mnv;
+    }
+    template <class X>
+    __device__ static float finish(const W &w, const X &x, float qlo, float qhi) {
+        float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
+        int j = x.c >> 1;
+        float sl, ml, sh, mh;
+        scale_min(w.hdr, 2 * j, sl, ml);
+        scale_min(w.hdr, 2 * j + 1, sh, mh);
+        float r = (d * sl) * qlo;
+        r = fmaf(d * sh, qhi, r);
+        r = fmaf(-(dmin * ml), x.slo, r);
+        r = fmaf(-(dmin * mh), x.shi, r);
+        return r;
+    }
+    __device__ static float dot(const W &w, const XF &x) {
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            l0 = fmaf(cvt_b0(lo), x.lo[i].x, l0);
+            l1 = fmaf(cvt_b1(lo), x.lo[i].y, l1);
+            l0 = fmaf(cvt_b2(lo), x.lo[i].z, l0);
+            l1 = fmaf(cvt_b3(lo), x.lo[i].w, l1);
+            h0 = fmaf(cvt_b0(hi), x.hi[i].x, h0);
+            h1 = fmaf(cvt_b1(hi), x.hi[i].y, h1);
+            h0 = fmaf(cvt_b2(hi), x.hi[i].z, h0);
+            h1 = fmaf(cvt_b3(hi), x.hi[i].w, h1);
+        }
+        return finish(w, x, l0 + l1, h0 + h1);
+    }
+    __device__ static float dot(const W &w, const XH &x) {
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        const jh2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t u = q[i];
+            jh2 a = as_h2((u & 0x000f000fu) | 0x64006400u) - off;
+            jh2 c = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - off;
+            jh2 b = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - off;
+            jh2 e = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - off;
+            l0 = dot2(a, x.lo[2 * i], l0);
+            l1 = dot2(c, x.lo[2 * i + 1], l1);
+            h0 = dot2(b, x.hi[2 * i], h0);
+            h1 = dot2(e, x.hi[2 * i + 1], h1);
+        }
+        return finish(w, x, l0 + l1, h0 + h1);
+    }
+};
+
+// ---- F16 weights: a unit is 8 binary16 weights (one 16-byte load) ----------
+struct FF16 {
+    static constexpr int UNIT = 8;
+    static constexpr bool PERM = false;
+    struct W { uint4 q; };
+    __device__ static W load(WPtr w, size_t unit) {
+        W r;
+        r.q = ld_stream((const uint4 *)w.qs + unit);
+        return r;
+    }
+    struct XF { jf4 a, b; };
+    __device__ static XF loadx(const float *xs, const float *, int u) {
+        const jf4 *p = (const jf4 *)(xs + (u >> 2) * XLayout<float>::STRIDE + (u & 3) * 8);
+        XF r;
+        r.a = p[0];
+        r.b = p[1];
+        return r;
+    }
+    struct XH { uint4 v; };
+    __device__ static XH loadx(const _Float16 *xs, const float *, int u) {
+        XH r;
+        r.v = *(const uint4 *)(xs + (u >> 2) * XLayout<_Float16>::STRIDE + (u & 3) * 8);
+        return r;
+    }
+    __device__ static float dot(const W &w, const XF &x) {
+        jh2 p0 = as_h2(w.q.x), p1 = as_h2(w.q.y), p2 = as_h2(w.q.z), p3 = as_h2(w.q.w);
+        float s0 = (float)p0.x * x.a.x;
+        float s1 = (float)p0.y * x.a.y;
+        s0 = fmaf((float)p1.x, x.a.z, s0);
+        s1 = fmaf((float)p1.y, x.a.w, s1);
+        s0 = fmaf((float)p2.x, x.b.x, s0);
+        s1 = fmaf((float)p2.y, x.b.y, s1);
+        s0 = fmaf((float)p3.x, x.b.z, s0);
+        s1 = fmaf((float)p3.y, x.b.w, s1);
+        return s0 + s1;
+    }
+    __device__ static float dot(const W &w, const XH &x) {
+        float s = dot2(as_h2(w.q.x), as_h2(x.v.x), 0.0f);
+        s = dot2(as_h2(w.q.y), as_h2(x.v.y), s);
+        s = dot2(as_h2(w.q.z), as_h2(x.v.z), s);
+        return dot2(as_h2(w.q.w), as_h2(x.v.w), s);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// cross-lane reduction of R row partials over LPR lanes
+// ---------------------------------------------------------------------------
+// On return, lanes whose (li % (LPR/R)) == 0 hold the total of row `ridx`.
+template <int LPR, int R>
+__device__ __forceinline__ float reduce_rows(float (&v)[R], int li, int &ridx) {
+    int base = 0;
+#pragma unroll
+    for (int c = R, o = LPR / 2; c > 1; c >>= 1, o >>= 1) {
+        const bool upper = (li & o) != 0;
+#pragma unroll
+        for (int j = 0; j < c / 2; ++j) {
+            float send = upper ? v[j] : v[j + c / 2];
+            float keep = upper ? v[j + c / 2] : v[j];
+            v[j] = keep + shfl_xor(send, o);
+        }
+        if (upper) base += c / 2;
+    }
+    float s = v[0];
+#pragma unroll
+    for (int o = LPR / (2 * R); o > 0; o >>= 1) s += shfl_xor(s, o);
+    ridx = base;
+    return s;
+}
+
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1 };
+
+struct GemvArgs {
+    WPtr w;
+    const void *x;       // activation [k]
+    void *y;             // output [n]
+    const float *resid;  // residual [n] (EPI_RESIDUAL)
+    uint32_t n, k;
+    uint32_t units;      // units per row
+    int out_f16;
+    int epi;
+};
+
+template <class F, typename XIN, typename XT, int LPR, int R, int BPL_MAX>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    XT *xs = (XT *)smem;
+    float *sx16 = (float *)(smem + ((nblk * XLayout<XT>::STRIDE * sizeof(XT) + 15) & ~15u));
+
+    constexpr int SUB = 64 / LPR;   // row groups per wavefront
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane % LPR, sg = lane / LPR;
+    const int waves = blockDim.x >> 6;
+    const uint32_t rows_per_wave = SUB * R;
+    const uint32_t wave_id = blockIdx.x * waves + wave;
+    const uint32_t row0 = wave_id * rows_per_wave + sg * R;
+    const int units = (int)a.units;
+
+    // Issue the weight loads first: they do not depend on x.
+    typename F::W wr[BPL_MAX][R];
+#pragma unroll
+    for (int i = 0; i < BPL_MAX; ++i) {
+        int u = li + i * LPR;
+        if (u < units) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t row = row0 + r;
+                row = row < a.n ? row : a.n - 1;
+                wr[i][r] = F::load(a.w, (size_t)row * units + u);
+            }
+        }
+    }
+
+    stage_x<XIN, XT, F::PERM && sizeof(XT) == 2>((const XIN *)a.x, a.k, xs, sx16);
+    __syncthreads();
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < BPL_MAX; ++i) {
+        int u = li + i * LPR;
+        if (u < units) {
+            auto xr = F::loadx((const XT *)xs, sx16, u);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] += F::dot(wr[i][r], xr);
+        }
+    }
+
+    int ridx;
+    float s = reduce_rows<LPR, R>(acc, li, ridx);
+    uint32_t row = row0 + ridx;
+    if ((li % (LPR / R)) == 0 && row < a.n) {
+        if (a.epi == EPI_RESIDUAL) s += a.resid[row];
+        if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
+        else ((float *)a.y)[row] = s;
+    }
+}
+
+// Generic fallback for F16 weights whose k is not a multiple of 8: one
+// wavefront per row, scalar loads (the tiny-model ffn_down case, k = 688).
+template <typename XIN>
+__global__ __launch_bounds__(256) void gemv_f16_any_kernel(GemvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= a.n) return;
+    const uint16_t *w = (const uint16_t *)a.w.qs + (size_t)row * a.k;
+    const XIN *x = (const XIN *)a.x;
+    float s = 0.0f;
+    for (uint32_t i = lane; i < a.k; i += 64) s = fmaf(h2f(w[i]), (float)x[i], s);
+    s = wave_sum(s);
+    if (lane == 0) {
+        if (a.epi == EPI_RESIDUAL) s += a.resid[row];
+        if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
+        else ((float *)a.y)[row] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launch selection
+// ---------------------------------------------------------------------------
+
+template <class F, typename XIN, typename XT, int LPR, int R, int BPL>
+int launch_one(janus_ctx *ctx, const GemvArgs &a) {
+    const int threads = 256, waves = threads / 64;
+    const uint32_t rows_per_block = (uint32_t)waves * (64 / LPR) * R;
+    const uint32_t grid = (a.n + rows_per_block - 1) / rows_per_block;
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    size_t lds = ((nblk * XLayout<XT>::STRIDE * sizeof(XT) + 15) & ~(size_t)15) + ((a.k + 15) / 16) * 4;
+    if (lds > 160 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
+    static bool attr_set = false;   // allow > 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU)
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void *)gemv_kernel<F, XIN, XT, LPR, R, BPL>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemv_kernel<F, XIN, XT, LPR, R, BPL>), dim3(grid), dim3(threads), lds, ctx->stream, a);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// Chooses lanes-per-row, rows-per-wave and the unrolled units-per-lane bound
+// from the row length. Large rows use the whole wavefront per row.
+template <class F, typename XIN, typename XT>
+int launch_fmt(janus_ctx *ctx, const GemvArgs &a) {
+    const int u = (int)a.units;
+    if (u <= 8) return launch_one<F, XIN, XT, 8, 4, 1>(ctx, a);
+    if (u <= 16) return launch_one<F, XIN, XT, 16, 4, 1>(ctx, a);
+    if (u <= 64) return launch_one<F, XIN, XT, 64, 4, 1>(ctx, a);
+    if (u <= 128) return launch_one<F, XIN, XT, 64, 4, 2>(ctx, a);
+    if (u <= 256) return launch_one<F, XIN, XT, 64, 2, 4>(ctx, a);
+    if (u <= 512) return launch_one<F, XIN, XT, 64, 2, 8>(ctx, a);
+    if (u <= 1024) return launch_one<F, XIN, XT, 64, 1, 16>(ctx, a);
+    if (u <= 2048) return launch_one<F, XIN, XT, 64, 1, 32>(ctx, a);
+    return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: row too long");
+}
+
+template <class F>
+int launch_gemv(janus_ctx *ctx, GemvArgs a, int x_dt) {
+    if (x_dt == JANUS_DT_F16) return launch_fmt<F, _Float16, _Float16>(ctx, a);
+    return launch_fmt<F, float, float>(ctx, a);
+}
+
+}  // namespace
+
+namespace janus {
+
+int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
+                  const float *residual) {
+    GemvArgs a;
+    a.w.qs = w->qs;
+    a.w.sc = w->sc;
+    a.x = x;
+    a.y = y;
+    a.resid = residual;
+    a.n = w->n;
+    a.k = w->k;
+    a.out_f16 = (y_dt == JANUS_DT_F16);
+    a.epi = residual ? EPI_RESIDUAL : EPI_STORE;
+    switch (w->type) {
+    case JANUS_DT_Q4_0: a.units = w->k / 32; return launch_gemv<FQ4_0>(ctx, a, x_dt);
+    case JANUS_DT_Q8_0: a.units = w->k / 32; return launch_gemv<FQ8_0>(ctx, a, x_dt);
+    case JANUS_DT_Q4_K: a.units = w->k / 32; return launch_gemv<FQ4_K>(ctx, a, x_dt);
+    case JANUS_DT_F16:
+        if (w->k % 8 == 0) {
+            a.units = w->k / 8;
+            return launch_gemv<FF16>(ctx, a, x_dt);
+        } else {
+            a.units = 0;
+            const uint32_t grid = (w->n + 3) / 4;
+            if (x_dt == JANUS_DT_F16)
+                hipLaunchKernelGGL(gemv_f16_any_kernel<_Float16>, dim3(grid), dim3(256), 0, ctx->stream, a);
+            else
+                hipLaunchKernelGGL(gemv_f16_any_kernel<float>, dim3(grid), dim3(256), 0, ctx->stream, a);
+            JANUS_LAUNCH_CHECK(ctx);
+            return JANUS_OK;
+        }
+    default:
+        return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE,
+                    "FATAL: No compute kernel bound for tensor type " + std::to_string(w->type));
+    }
+}
+
+}  // namespace janus

@@ -1,0 +1,251 @@
+// glue.hip -- normalisation, activation, RoPE, KV append, embedding and
+// greedy-sampling kernels around the matrix products.
+//
+// Reference kernels (crates/janus-engine/src/compute/shaders/):
+// activations.wgsl (rmsnorm :67-134, silu :20-35), elementwise_mul.wgsl,
+// add_tensors.wgsl, rope.wgsl, update_cache.wgsl, embed.wgsl, argmax.wgsl;
+// sampler penalty: model/sampler.rs:599-613.
+#include "internal.h"
+
+namespace janus {
+
+// ---- RMSNorm: one workgroup per row ---------------------------------------
+// y = (x / sqrt(sum(x^2)/H + eps)) * gamma  -- division by the root, as the
+// reference writes it (activations.wgsl:114,128).
+template <bool OUT_F16>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ in, void *__restrict__ out,
+                                                      const float *__restrict__ gamma, uint32_t hidden,
+                                                      float eps) {
+    __shared__ float red[4];
+    const float *x = in + (size_t)blockIdx.x * hidden;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) s = fmaf(x[i], x[i], s);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
+    const float rms = sqrtf(tot / (float)hidden + eps);
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
+        float v = (x[i] / rms) * gamma[i];
+        if (OUT_F16) ((uint16_t *)out)[(size_t)blockIdx.x * hidden + i] = f2h_bits(v);
+        else ((float *)out)[(size_t)blockIdx.x * hidden + i] = v;
+    }
+}
+
+int rmsnorm_launch(janus_ctx *ctx, const float *in, void *out, int out_dt, const float *gamma,
+                   uint32_t batch, uint32_t hidden, float eps) {
+    if (out_dt == JANUS_DT_F16)
+        hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// ---- elementwise ------------------------------------------------------------
+__device__ __forceinline__ float silu_f(float x) { return x * (1.0f / (1.0f + expf(-x))); }
+
+template <int OP, bool OUT_F16>
+__global__ __launch_bounds__(256) void elementwise_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                                          void *__restrict__ out, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v;
+    if (OP == EW_SILU) v = silu_f(a[i]);
+    else if (OP == EW_MUL) v = a[i] * b[i];
+    else if (OP == EW_ADD) v = a[i] + b[i];
+    else v = silu_f(a[i]) * b[i];
+    if (OUT_F16) ((uint16_t *)out)[i] = f2h_bits(v);
+    else ((float *)out)[i] = v;
+}
+
+int elementwise_launch(janus_ctx *ctx, int op, const float *a, const float *b, void *out, int out_dt,
+                       uint32_t n) {
+    dim3 grid((n + 255) / 256), block(256);
+    bool h = out_dt == JANUS_DT_F16;
+    switch (op) {
+    case EW_SILU: hipLaunchKernelGGL((elementwise_kernel<EW_SILU, false>), grid, block, 0, ctx->stream, a, b, out, n); break;
+    case EW_MUL: hipLaunchKernelGGL((elementwise_kernel<EW_MUL, false>), grid, block, 0, ctx->stream, a, b, out, n); break;
+    case EW_ADD: hipLaunchKernelGGL((elementwise_kernel<EW_ADD, false>), grid, block, 0, ctx->stream, a, b, out, n); break;
+    default:
+        if (h) hipLaunchKernelGGL((elementwise_kernel<EW_SWIGLU, true>), grid, block, 0, ctx->stream, a, b, out, n);
+        else hipLaunchKernelGGL((elementwise_kernel<EW_SWIGLU, false>), grid, block, 0, ctx->stream, a, b, out, n);
+    }
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// ---- RoPE (half-split, host cos/sin table) ---------------------------------
+// One thread per (row, head, pair): y0 = x0*c - x1*s, y1 = x0*s + x1*c
+// (rope.wgsl:71-72). In-place is safe: each thread owns its pair.
+__global__ __launch_bounds__(256) void rope_kernel(const float *in, float *out, const float *__restrict__ table,
+                                                   uint32_t batch, uint32_t heads, uint32_t hd,
+                                                   uint32_t position, const int32_t *__restrict__ positions) {
+    const uint32_t half = hd / 2;
+    uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= batch * heads * half) return;
+    uint32_t b = idx / (heads * half), rem = idx % (heads * half);
+    uint32_t h = rem / half, i = rem % half;
+    uint32_t pos = positions ? (uint32_t)positions[b] : position;
+    size_t base = ((size_t)b * heads + h) * hd;
+    float x0 = in[base + i], x1 = in[base + i + half];
+    float c = table[((size_t)pos * half + i) * 2], s = table[((size_t)pos * half + i) * 2 + 1];
+    out[base + i] = x0 * c - x1 * s;
+    out[base + i + half] = x0 * s + x1 * c;
+}
+
+int rope_launch(janus_ctx *ctx, const float *in, float *out, const float *table, uint32_t batch, uint32_t heads,
+                uint32_t hd, uint32_t position, const int32_t *positions) {
+    uint32_t n = batch * heads * (hd / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, in, out, table, batch, heads,
+                       hd, position, positions);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// ---- KV append ----------------------------------------------------------------
+template <typename KV>
+__global__ __launch_bounds__(256) void kv_update_kernel(const float *__restrict__ k_new, const float *__restrict__ v_new,
+                                                        KV *__restrict__ kc, KV *__restrict__ vc, uint32_t batch,
+                                                        uint32_t row_elems, uint32_t position, uint32_t max_seq,
+                                                        const int32_t *__restrict__ row_base,
+                                                        const int32_t *__restrict__ positions) {
+    uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= batch * row_elems) return;
+    uint32_t b = idx / row_elems, e = idx % row_elems;
+    const uint32_t pos = positions ? (uint32_t)positions[b] : position;
+    if (pos >= max_seq) return;   // device-side positions past capacity are dropped
+    size_t row = (size_t)(row_base ? (uint32_t)row_base[b] : b * max_seq) + pos;
+    kc[row * row_elems + e] = (KV)k_new[idx];
+    vc[row * row_elems + e] = (KV)v_new[idx];
+}
+
+int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, void *kc, void *vc, int kv_dt,
+                     uint32_t batch, uint32_t row_elems, uint32_t position, uint32_t max_seq,
+                     const int32_t *row_base, const int32_t *positions) {
+    uint32_t n = batch * row_elems;
+    dim3 grid((n + 255) / 256), block(256);
+    if (kv_dt == JANUS_DT_F16)
+        hipLaunchKernelGGL(kv_update_kernel<_Float16>, grid, block, 0, ctx->stream, k_new, v_new, (_Float16 *)kc,
+                           (_Float16 *)vc, batch, row_elems, position, max_seq, row_base, positions);
+    else
+        hipLaunchKernelGGL(kv_update_kernel<float>, grid, block, 0, ctx->stream, k_new, v_new, (float *)kc,
+                           (float *)vc, batch, row_elems, position, max_seq, row_base, positions);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// ---- embedding gather ---------------------------------------------------------
+// Token ids either travel as kernel arguments (host ids, up to 64 per launch)
+// or are read from device memory.
+struct EmbedIds {
+    int32_t id[64];
+};
+
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t *__restrict__ table, EmbedIds ids,
+                                                    const int32_t *__restrict__ d_ids, float *__restrict__ out,
+                                                    uint32_t hidden, uint32_t vocab) {
+    const uint32_t b = blockIdx.y;
+    const int32_t id = d_ids ? d_ids[b] : ids.id[b];
+    float *o = out + (size_t)b * hidden;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+        o[i] = ((uint32_t)id < vocab) ? h2f(table[(size_t)id * hidden + i]) : 0.0f;
+}
+
+int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
+                 uint32_t batch, float *out) {
+    const uint32_t hidden = table->k, vocab = table->n;
+    const uint32_t gx = (hidden + 255) / 256 < 16 ? (hidden + 255) / 256 : 16;
+    for (uint32_t b0 = 0; b0 < batch; b0 += 64) {
+        uint32_t nb = batch - b0 < 64 ? batch - b0 : 64;
+        EmbedIds ids;
+        std::memset(&ids, 0, sizeof(ids));
+        if (h_ids)
+            for (uint32_t i = 0; i < nb; ++i) ids.id[i] = (int32_t)h_ids[b0 + i];
+        hipLaunchKernelGGL(embed_kernel, dim3(gx, nb), dim3(256), 0, ctx->stream, (const uint16_t *)table->qs, ids,
+                           d_ids ? d_ids + b0 : nullptr, out + (size_t)b0 * hidden, hidden, vocab);
+        JANUS_LAUNCH_CHECK(ctx);
+    }
+    return JANUS_OK;
+}
+
+// ---- greedy argmax --------------------------------------------------------------
+// TIE_LAST: the last maximal index (Iterator::max_by, model/sampler.rs:784-795);
+// NaN entries never win. TIE_WGSL: the 256-lane scan and strict '>' tree of
+// argmax.wgsl:26-126 reproduced lane for lane.
+__global__ __launch_bounds__(1024) void argmax_last_kernel(const float *__restrict__ logits, int32_t *__restrict__ out,
+                                                           uint32_t vocab) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    const float *l = logits + (size_t)blockIdx.x * vocab;
+    float bv = -INFINITY;
+    int32_t bi = -1;
+    for (uint32_t i = threadIdx.x; i < vocab; i += blockDim.x) {
+        float v = l[i];
+        if (v > bv || (v == bv && (int32_t)i > bi)) { bv = v; bi = (int32_t)i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = shfl_xor(bv, o);
+        int32_t oi = shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+            if (sv[w] > bv || (sv[w] == bv && si[w] > bi)) { bv = sv[w]; bi = si[w]; }
+        out[blockIdx.x] = bi < 0 ? 0 : bi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_wgsl_kernel(const float *__restrict__ logits, int32_t *__restrict__ out,
+                                                          uint32_t vocab) {
+    __shared__ float sv[256];
+    __shared__ int32_t si[256];
+    const float *l = logits + (size_t)blockIdx.x * vocab;
+    const uint32_t t = threadIdx.x;
+    float mv = -1e38f;
+    int32_t mi = 0;
+    for (uint32_t i = t; i < vocab; i += 256)
+        if (l[i] > mv) { mv = l[i]; mi = (int32_t)i; }
+    sv[t] = mv;
+    si[t] = mi;
+    __syncthreads();
+    for (uint32_t stride = 128; stride >= 2; stride >>= 1) {
+        if (t < stride && sv[t + stride] > sv[t]) { sv[t] = sv[t + stride]; si[t] = si[t + stride]; }
+        __syncthreads();
+    }
+    if (t == 0) out[blockIdx.x] = sv[1] > sv[0] ? si[1] : si[0];
+}
+
+int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie) {
+    if (tie == JANUS_TIE_WGSL)
+        hipLaunchKernelGGL(argmax_wgsl_kernel, dim3(batch), dim3(256), 0, ctx->stream, logits, out, vocab);
+    else
+        hipLaunchKernelGGL(argmax_last_kernel, dim3(batch), dim3(1024), 0, ctx->stream, logits, out, vocab);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// Sequential in context order so repeated ids compound exactly as the host loop.
+__global__ void penalty_kernel(float *logits, uint32_t vocab, const int32_t *__restrict__ ctx_ids, uint32_t n,
+                               float penalty) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t t = (uint32_t)ctx_ids[i];
+        if (t < vocab) {
+            float v = logits[t];
+            logits[t] = v > 0.0f ? v / penalty : v * penalty;
+        }
+    }
+}
+
+int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t *ids, uint32_t n, float penalty) {
+    hipLaunchKernelGGL(penalty_kernel, dim3(1), dim3(64), 0, ctx->stream, logits, vocab, ids, n, penalty);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+}  // namespace janus

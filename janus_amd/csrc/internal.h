@@ -1,0 +1,150 @@
+// internal.h -- shared host/device definitions of libjanus_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "../../include/janus_hip.h"
+
+// ---------------------------------------------------------------------------
+// host-side context and weight handles
+// ---------------------------------------------------------------------------
+
+struct janus_ctx {
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string last_error;
+    // Attention split-K partials; grows on first use and is then reused.
+    void *attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+};
+
+// HBM layout of an uploaded weight. Rows are the output dimension n.
+//  Q4_0 : qs  = n * nb * 16 bytes (GGML nibble order per block), 16-B aligned
+//         sc  = n * nb binary16 scales (nb = k / 32)
+//  Q8_0 : qs  = n * nb * 32 bytes (int8), sc = n * nb binary16 scales
+//  Q4_K : qs  = the GGML 144-byte super-blocks, unchanged, 256-B aligned base
+//  F16  : qs  = n * k binary16, row-major, FTZ applied at upload when flagged
+struct janus_weight {
+    int type = 0;
+    uint32_t n = 0, k = 0;
+    uint32_t flags = 0;
+    void *base = nullptr;     // single allocation
+    size_t bytes = 0;
+    const uint8_t *qs = nullptr;
+    const uint16_t *sc = nullptr;
+};
+
+namespace janus {
+
+// Records `msg` as the context's last error and returns `code`.
+int fail(janus_ctx *ctx, int code, const std::string &msg);
+int hip_fail(janus_ctx *ctx, hipError_t e, const char *what);
+
+#define JANUS_HIP_CHECK(ctx, expr)                                  \
+    do {                                                            \
+        hipError_t _e = (expr);                                     \
+        if (_e != hipSuccess) return ::janus::hip_fail(ctx, _e, #expr); \
+    } while (0)
+
+#define JANUS_LAUNCH_CHECK(ctx)                                     \
+    do {                                                            \
+        hipError_t _e = hipGetLastError();                          \
+        if (_e != hipSuccess) return ::janus::hip_fail(ctx, _e, "kernel launch"); \
+    } while (0)
+
+inline bool is_act_dtype(int dt) { return dt == JANUS_DT_F32 || dt == JANUS_DT_F16; }
+inline size_t act_bytes(int dt) { return dt == JANUS_DT_F16 ? 2 : 4; }
+
+// Grows the context's attention workspace to at least `bytes`.
+int ensure_attn_ws(janus_ctx *ctx, size_t bytes);
+// Returns JANUS_E_NO_DEVICE for a validation-only context (device < 0).
+int need_device(janus_ctx *ctx);
+
+// M = 1 product (gemv.hip). residual may be null; when set, y must be F32.
+int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
+                  const float *residual);
+// rows >= 1 product (small-M MFMA GEMM for rows > 1).
+int gemm_dispatch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w, void *c,
+                  int c_dt, uint32_t rows, const float *residual);
+int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w, void *c, int c_dt,
+                       uint32_t rows, const float *residual);
+
+enum { EW_SILU = 0, EW_MUL = 1, EW_ADD = 2, EW_SWIGLU = 3 };
+int rmsnorm_launch(janus_ctx *ctx, const float *in, void *out, int out_dt, const float *gamma, uint32_t batch,
+                   uint32_t hidden, float eps);
+int elementwise_launch(janus_ctx *ctx, int op, const float *a, const float *b, void *out, int out_dt, uint32_t n);
+int rope_launch(janus_ctx *ctx, const float *in, float *out, const float *table, uint32_t batch, uint32_t heads,
+                uint32_t hd, uint32_t position, const int32_t *positions);
+int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, void *kc, void *vc, int kv_dt,
+                     uint32_t batch, uint32_t row_elems, uint32_t position, uint32_t max_seq,
+                     const int32_t *row_base, const int32_t *positions);
+// Attention split sizing shared by the launch and workspace reservation.
+void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t kv_heads, uint32_t max_len, uint32_t *chunk,
+                    uint32_t *splits);
+int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                      uint32_t max_len);
+int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, float *out,
+                     uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
+                     uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
+                     float scale);
+int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
+                 uint32_t batch, float *out);
+int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie);
+int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t *ids, uint32_t n, float penalty);
+
+}  // namespace janus
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+typedef _Float16 jh2 __attribute__((ext_vector_type(2)));
+typedef _Float16 jh4 __attribute__((ext_vector_type(4)));
+typedef float jf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t ju4 __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming load (non-temporal: weights are read once per launch).
+__device__ __forceinline__ uint4 ld_stream(const void *p) {
+    ju4 v = __builtin_nontemporal_load((const ju4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Exact binary16 -> binary32 (subnormals kept). Hardware conversion is exact
+// with f16 denormals enabled (the gfx950 default for HIP).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Q8_0 scale decode of shaders/gemm_q8_0.wgsl:33-60: exact, but exponent 31
+// (inf/nan) becomes +-1e38.
+__device__ __forceinline__ float h2f_q8(uint16_t h) {
+    float v = h2f(h);
+    return ((h & 0x7c00u) == 0x7c00u) ? ((h & 0x8000u) ? -1e38f : 1e38f) : v;
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);  // round to nearest even
+}
+
+template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+// Sum over all 64 lanes of a wavefront; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
+    return v;
+}

@@ -1,0 +1,404 @@
+// model.hip -- the C++ decode driver (include/janus_model.h).
+//
+// Reference call stack mirrored here (crates/janus-engine/src/):
+//   Model::forward            model/transformer/forward.rs:25-119
+//   TransformerBlock::forward model/block.rs:190-458 (op order per layer)
+//   Model::generate           model/transformer/generation.rs:129-323
+//   Sampler::sample (greedy)  model/sampler.rs:146-209, 599-613, 784-795
+// Differences by design: the o-proj and down-proj residual adds are fused
+// into the products' epilogues (same f32 addition), SiLU and the gate*up
+// product are one kernel, K/V may be stored as binary16, and every sequence
+// of a batch carries its own position (the reference shares one, rope.wgsl:64-66).
+#include <cmath>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/janus_model.h"
+#include "internal.h"
+
+using namespace janus;
+
+struct janus_model {
+    janus_ctx *ctx = nullptr;
+    janus_model_config cfg{};
+    struct Layer {
+        float *attn_norm = nullptr, *ffn_norm = nullptr;
+        janus_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        janus_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+    };
+    std::vector<Layer> layers;
+    janus_weight *tok_embd = nullptr, *lm_head = nullptr;
+    float *out_norm = nullptr;
+    // activations (max_batch rows each)
+    float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h1 = nullptr;
+    float *gate = nullptr, *up = nullptr, *logits = nullptr;
+    void *xn = nullptr, *act = nullptr;   // act_dtype
+    void *kcache = nullptr, *vcache = nullptr;
+    size_t layer_kv_elems = 0;
+    float *rope = nullptr;
+    int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_gen = nullptr;
+    std::vector<uint32_t> h_pos;   // graph mode: host mirror of device positions
+    uint32_t graph_nseq = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+};
+
+namespace {
+
+size_t kv_elem_bytes(int dt) { return dt == JANUS_DT_F16 ? 2 : 4; }
+
+int parse_layer_name(const std::string &name, uint32_t *layer, std::string *rest) {
+    if (name.rfind("blk.", 0) != 0) return 0;
+    size_t dot = name.find('.', 4);
+    if (dot == std::string::npos) return 0;
+    *layer = (uint32_t)std::stoul(name.substr(4, dot - 4));
+    *rest = name.substr(dot + 1);
+    return 1;
+}
+
+__global__ void lens_from_pos_kernel(const int32_t *pos, int32_t *lens, uint32_t n) {
+    uint32_t i = threadIdx.x;
+    if (i < n) lens[i] = pos[i] + 1;
+}
+
+__global__ void advance_pos_kernel(int32_t *pos, int32_t *lens, uint32_t n) {
+    uint32_t i = threadIdx.x;
+    if (i < n) {
+        pos[i] += 1;
+        lens[i] = pos[i] + 1;
+    }
+}
+
+// One decode step over nseq rows whose ids are either host ids or device ids
+// and whose positions / lengths are already in d_pos / d_lens.
+int forward_rows(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t nseq, uint32_t max_len) {
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const uint32_t kvd = c.kv_heads * c.head_dim;
+    int e;
+    if ((e = embed_launch(ctx, m->tok_embd, h_ids, d_ids, nseq, m->hidden))) return e;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const janus_model::Layer &L = m->layers[l];
+        void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        // attention block (block.rs:223-355)
+        if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, c.act_dtype, L.attn_norm, nseq, c.hidden, c.rms_eps))) return e;
+        if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.q, m->q, JANUS_DT_F32, nseq, nullptr))) return e;
+        if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.k, m->k, JANUS_DT_F32, nseq, nullptr))) return e;
+        if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.v, m->v, JANUS_DT_F32, nseq, nullptr))) return e;
+        if ((e = rope_launch(ctx, m->q, m->q, m->rope, nseq, c.heads, c.head_dim, 0, m->d_pos))) return e;
+        if ((e = rope_launch(ctx, m->k, m->k, m->rope, nseq, c.kv_heads, c.head_dim, 0, m->d_pos))) return e;
+        if ((e = kv_update_launch(ctx, m->k, m->v, kc, vc, c.kv_dtype, nseq, kvd, 0, c.max_seq_len, nullptr,
+                                  m->d_pos)))
+            return e;
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn, nseq, c.heads, c.kv_heads, c.head_dim, 0,
+                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim))))
+            return e;
+        // o-proj with the residual add fused: h1 = hidden + attn . Wo^T
+        if ((e = gemm_dispatch(ctx, m->attn, JANUS_DT_F32, L.o, m->h1, JANUS_DT_F32, nseq, m->hidden))) return e;
+        // feed-forward block (block.rs:370-447)
+        if ((e = rmsnorm_launch(ctx, m->h1, m->xn, c.act_dtype, L.ffn_norm, nseq, c.hidden, c.rms_eps))) return e;
+        if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.gate, m->gate, JANUS_DT_F32, nseq, nullptr))) return e;
+        if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.up, m->up, JANUS_DT_F32, nseq, nullptr))) return e;
+        if ((e = elementwise_launch(ctx, EW_SWIGLU, m->gate, m->up, m->act, c.act_dtype, nseq * c.ffn))) return e;
+        if ((e = gemm_dispatch(ctx, m->act, c.act_dtype, L.down, m->hidden, JANUS_DT_F32, nseq, m->h1))) return e;
+    }
+    // final norm + LM head (forward.rs:87-111)
+    if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, c.act_dtype, m->out_norm, nseq, c.hidden, c.rms_eps))) return e;
+    return gemm_dispatch(ctx, m->xn, c.act_dtype, m->lm_head, m->logits, JANUS_DT_F32, nseq, nullptr);
+}
+
+struct Positions {
+    int32_t p[64];
+};
+
+// Positions travel as kernel arguments, so the update is ordered on the
+// stream behind any still-running step that reads the previous values.
+__global__ void set_positions_kernel(Positions pos, int32_t *d_pos, int32_t *d_lens, uint32_t n) {
+    uint32_t i = threadIdx.x;
+    if (i < n) {
+        d_pos[i] = pos.p[i];
+        d_lens[i] = pos.p[i] + 1;
+    }
+}
+
+int upload_positions(janus_model *m, const uint32_t *positions, uint32_t nseq) {
+    Positions p;
+    std::memset(&p, 0, sizeof(p));
+    for (uint32_t i = 0; i < nseq; ++i) p.p[i] = (int32_t)positions[i];
+    hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(64), 0, m->ctx->stream, p, m->d_pos, m->d_lens, nseq);
+    JANUS_LAUNCH_CHECK(m->ctx);
+    return JANUS_OK;
+}
+
+void free_graph(janus_model *m) {
+    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) hipGraphDestroy(m->graph);
+    m->graph_exec = nullptr;
+    m->graph = nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_model **out) {
+    if (!ctx || !cfg || !out) return JANUS_E_INVALID_ARG;
+    *out = nullptr;
+    const janus_model_config &c = *cfg;
+    if (!c.hidden || !c.heads || !c.kv_heads || !c.head_dim || !c.ffn || !c.vocab || !c.layers || !c.max_seq_len)
+        return fail(ctx, JANUS_E_INVALID_DIM, "model: zero dimension in config");
+    if (c.heads % c.kv_heads) return fail(ctx, JANUS_E_INVALID_DIM, "model: heads must be a multiple of kv_heads");
+    if (c.head_dim * c.heads != c.hidden) return fail(ctx, JANUS_E_INVALID_DIM, "model: head_dim * heads != hidden");
+    if (c.max_batch == 0 || c.max_batch > 64) return fail(ctx, JANUS_E_INVALID_DIM, "model: max_batch must be 1..64");
+    if (!is_act_dtype(c.kv_dtype) || !is_act_dtype(c.act_dtype))
+        return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "model: kv/act dtype must be F32 or F16");
+    if (int e = need_device(ctx)) return e;
+    janus_model *m = new janus_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->layers.resize(c.layers);
+    const size_t B = c.max_batch, kvd = (size_t)c.kv_heads * c.head_dim;
+    auto alloc = [&](void **p, size_t bytes) { return hipMalloc(p, bytes < 256 ? 256 : bytes) == hipSuccess; };
+    bool ok = alloc((void **)&m->hidden, B * c.hidden * 4) && alloc((void **)&m->q, B * c.hidden * 4) &&
+              alloc((void **)&m->k, B * kvd * 4) && alloc((void **)&m->v, B * kvd * 4) &&
+              alloc((void **)&m->attn, B * c.hidden * 4) && alloc((void **)&m->h1, B * c.hidden * 4) &&
+              alloc((void **)&m->gate, B * c.ffn * 4) && alloc((void **)&m->up, B * c.ffn * 4) &&
+              alloc((void **)&m->logits, B * c.vocab * 4) && alloc(&m->xn, B * c.hidden * 4) &&
+              alloc(&m->act, B * c.ffn * 4) &&
+              alloc((void **)&m->rope, (size_t)c.max_seq_len * c.head_dim * 4) &&
+              alloc((void **)&m->d_pos, B * 4) && alloc((void **)&m->d_lens, B * 4) &&
+              alloc((void **)&m->d_tokens, B * 4) && alloc((void **)&m->d_gen, (size_t)c.max_seq_len * 4);
+    m->layer_kv_elems = B * c.max_seq_len * kvd;
+    size_t kv_bytes = (size_t)c.layers * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+    ok = ok && alloc(&m->kcache, kv_bytes) && alloc(&m->vcache, kv_bytes);
+    if (!ok) {
+        janus_model_destroy(m);
+        return fail(ctx, JANUS_E_OOM, "model: device allocation failed");
+    }
+    if (int e = janus_rope_table(ctx, m->rope, c.max_seq_len, c.head_dim, c.rope_theta)) {
+        janus_model_destroy(m);
+        return e;
+    }
+    if (int e = attention_reserve(ctx, c.max_batch, c.heads, c.kv_heads, c.head_dim, c.max_seq_len)) {
+        janus_model_destroy(m);
+        return e;
+    }
+    *out = m;
+    return JANUS_OK;
+}
+
+void janus_model_destroy(janus_model *m) {
+    if (!m) return;
+    hipStreamSynchronize(m->ctx->stream);
+    free_graph(m);
+    for (auto &L : m->layers) {
+        for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) janus_weight_free(m->ctx, w);
+        hipFree(L.attn_norm);
+        hipFree(L.ffn_norm);
+    }
+    janus_weight_free(m->ctx, m->tok_embd);
+    janus_weight_free(m->ctx, m->lm_head);
+    for (void *p : {(void *)m->out_norm, (void *)m->hidden, (void *)m->q, (void *)m->k, (void *)m->v,
+                    (void *)m->attn, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
+                    m->act, m->kcache, m->vcache, (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
+                    (void *)m->d_tokens, (void *)m->d_gen})
+        if (p) hipFree(p);
+    delete m;
+}
+
+int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t n, uint32_t k, const void *bytes,
+                           size_t nbytes) {
+    if (!m || !cname || !bytes) return JANUS_E_INVALID_ARG;
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const std::string name(cname);
+    auto set_vec = [&](float **dst, uint32_t len) -> int {
+        if (type != JANUS_DT_F32 || k != 0 || n != len || nbytes != (size_t)len * 4)
+            return fail(ctx, JANUS_E_INVALID_DIM, name + ": expected F32 vector of " + std::to_string(len));
+        if (!*dst) JANUS_HIP_CHECK(ctx, hipMalloc((void **)dst, (size_t)len * 4));
+        JANUS_HIP_CHECK(ctx, hipMemcpy(*dst, bytes, nbytes, hipMemcpyHostToDevice));
+        return JANUS_OK;
+    };
+    auto set_w = [&](janus_weight **dst, uint32_t rows, uint32_t cols, uint32_t flags) -> int {
+        if (n != rows || k != cols)
+            return fail(ctx, JANUS_E_INVALID_DIM, name + ": expected [" + std::to_string(rows) + "x" +
+                                                      std::to_string(cols) + "]");
+        // 2-D float weights follow allocate_tensors: binary16 storage decoded with
+        // f16_to_f32_safe (shaders/gemm.wgsl:18-31, embed.wgsl:11-20).
+        if (type == JANUS_DT_F32 || type == JANUS_DT_F16) flags |= JANUS_WEIGHT_FTZ_F16;
+        if (type == JANUS_DT_Q4_K) flags |= JANUS_WEIGHT_FTZ_F16;   // gemm_q4_k.wgsl:62-65
+        janus_weight *w = nullptr;
+        if (int e = janus_weight_upload(ctx, type, n, k, bytes, nbytes, flags, &w)) return e;
+        janus_weight_free(ctx, *dst);
+        *dst = w;
+        return JANUS_OK;
+    };
+    free_graph(m);
+    if (name == "token_embd.weight") {
+        if (type != JANUS_DT_F32 && type != JANUS_DT_F16)
+            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "token_embd.weight must be F32 or F16");
+        return set_w(&m->tok_embd, c.vocab, c.hidden, 0);
+    }
+    if (name == "output_norm.weight") return set_vec(&m->out_norm, c.hidden);
+    if (name == "output.weight") {
+        // The LM head is always the f16 GEMM (model/transformer/forward.rs:101-111).
+        if (type != JANUS_DT_F32 && type != JANUS_DT_F16)
+            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "output.weight must be F32 or F16");
+        return set_w(&m->lm_head, c.vocab, c.hidden, 0);
+    }
+    uint32_t l;
+    std::string rest;
+    if (!parse_layer_name(name, &l, &rest) || l >= c.layers)
+        return fail(ctx, JANUS_E_INVALID_ARG, "unknown tensor " + name);
+    janus_model::Layer &L = m->layers[l];
+    const uint32_t kvd = c.kv_heads * c.head_dim;
+    if (rest == "attn_norm.weight") return set_vec(&L.attn_norm, c.hidden);
+    if (rest == "ffn_norm.weight") return set_vec(&L.ffn_norm, c.hidden);
+    if (rest == "attn_q.weight") return set_w(&L.q, c.hidden, c.hidden, 0);
+    if (rest == "attn_k.weight") return set_w(&L.k, kvd, c.hidden, 0);
+    if (rest == "attn_v.weight") return set_w(&L.v, kvd, c.hidden, 0);
+    if (rest == "attn_output.weight") return set_w(&L.o, c.hidden, c.hidden, 0);
+    if (rest == "ffn_gate.weight") return set_w(&L.gate, c.ffn, c.hidden, 0);
+    if (rest == "ffn_up.weight") return set_w(&L.up, c.ffn, c.hidden, 0);
+    if (rest == "ffn_down.weight") return set_w(&L.down, c.hidden, c.ffn, 0);
+    return fail(ctx, JANUS_E_INVALID_ARG, "unknown tensor " + name);
+}
+
+int janus_model_validate(janus_model *m) {
+    if (!m) return JANUS_E_INVALID_ARG;
+    if (!m->tok_embd || !m->lm_head || !m->out_norm) return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing global tensor");
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        const auto &L = m->layers[l];
+        if (!L.attn_norm || !L.ffn_norm || !L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down)
+            return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
+    }
+    return JANUS_OK;
+}
+
+int janus_model_reset(janus_model *m) {
+    if (!m) return JANUS_E_INVALID_ARG;
+    // KVCache::reset only rewinds the position; stale rows are never read
+    // because attention reads rows [0, pos + 1).
+    free_graph(m);
+    return JANUS_OK;
+}
+
+int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq) {
+    if (!m || !tokens || !positions) return JANUS_E_INVALID_ARG;
+    if (nseq == 0 || nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "forward: bad batch size");
+    if (int e = janus_model_validate(m)) return e;
+    uint32_t max_len = 0;
+    for (uint32_t i = 0; i < nseq; ++i) {
+        if (positions[i] >= m->cfg.max_seq_len)
+            return fail(m->ctx, JANUS_E_KV_OVERFLOW, "KV cache position " + std::to_string(positions[i]) +
+                                                         " exceeds max_seq_len " + std::to_string(m->cfg.max_seq_len));
+        if (tokens[i] >= m->cfg.vocab)
+            return fail(m->ctx, JANUS_E_TOKEN_RANGE, "Token ID " + std::to_string(tokens[i]) + " exceeds vocab size");
+        max_len = positions[i] + 1 > max_len ? positions[i] + 1 : max_len;
+    }
+    if (int e = upload_positions(m, positions, nseq)) return e;
+    return forward_rows(m, tokens, nullptr, nseq, max_len);
+}
+
+const float *janus_model_logits(const janus_model *m) { return m ? m->logits : nullptr; }
+
+void *janus_model_kv_cache(const janus_model *m, int which) {
+    if (!m) return nullptr;
+    return which == 0 ? m->kcache : m->vcache;
+}
+
+int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq) {
+    if (!m || !h_out) return JANUS_E_INVALID_ARG;
+    return janus_d2h(m->ctx, h_out, m->logits, (size_t)nseq * m->cfg.vocab * 4);
+}
+
+int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
+                         float penalty, uint32_t *out_tokens, uint32_t *n_out) {
+    if (!m || !prompt || !out_tokens || !n_out) return JANUS_E_INVALID_ARG;
+    *n_out = 0;
+    if (n_prompt == 0) return fail(m->ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
+    janus_ctx *ctx = m->ctx;
+    // prefill: one forward per prompt token (generation.rs:161-173)
+    uint32_t pos = 0;
+    for (uint32_t i = 0; i < n_prompt; ++i, ++pos)
+        if (int e = janus_model_forward(m, &prompt[i], &pos, 1)) return e;
+    uint32_t last = prompt[n_prompt - 1];
+    std::vector<int32_t> generated;
+    int32_t *d_choice = m->d_tokens;
+    for (uint32_t step = 0; step < max_tokens; ++step) {
+        if (pos >= m->cfg.max_seq_len) break;
+        // the first decode step re-feeds the last prompt token at position n (generation.rs:176,217)
+        if (int e = janus_model_forward(m, &last, &pos, 1)) return e;
+        // sample: penalty over the generated tokens, then the last-max argmax
+        if (!generated.empty()) {
+            JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_gen, generated.data(), generated.size() * 4,
+                                                hipMemcpyHostToDevice, ctx->stream));
+            if (int e = penalty_launch(ctx, m->logits, m->cfg.vocab, m->d_gen, (uint32_t)generated.size(), penalty))
+                return e;
+        }
+        if (int e = argmax_launch(ctx, m->logits, d_choice, m->cfg.vocab, 1, JANUS_TIE_LAST)) return e;
+        int32_t next = 0;
+        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&next, d_choice, 4, hipMemcpyDeviceToHost, ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        out_tokens[(*n_out)++] = (uint32_t)next;
+        if (next == 128001 || next == 128009) break;   // LLAMA3_END_OF_TEXT_ID / LLAMA3_EOT_ID
+        generated.push_back(next);
+        last = (uint32_t)next;
+        ++pos;
+    }
+    return JANUS_OK;
+}
+
+int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq) {
+    if (!m || !tokens || !positions) return JANUS_E_INVALID_ARG;
+    if (nseq == 0 || nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "graph: bad batch size");
+    janus_ctx *ctx = m->ctx;
+    // Eager step first: checks arguments, sets kernel attributes and grows
+    // workspaces outside of capture. It writes the same K/V rows the first
+    // replay rewrites.
+    if (int e = janus_model_forward(m, tokens, positions, nseq)) return e;
+    std::vector<int32_t> ids(tokens, tokens + nseq);
+    JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_tokens, ids.data(), nseq * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int e = upload_positions(m, positions, nseq)) return e;
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    m->h_pos.assign(positions, positions + nseq);
+    m->graph_nseq = nseq;
+    free_graph(m);
+    JANUS_HIP_CHECK(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int e = forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
+    if (!e) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
+    if (!e) {
+        hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq);
+        if (hipGetLastError() != hipSuccess) e = JANUS_E_HIP;
+    }
+    hipGraph_t g = nullptr;
+    hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
+    if (e) {
+        if (g) hipGraphDestroy(g);
+        return e;
+    }
+    if (ce != hipSuccess) return hip_fail(ctx, ce, "hipStreamEndCapture");
+    m->graph = g;
+    JANUS_HIP_CHECK(ctx, hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0));
+    return JANUS_OK;
+}
+
+int janus_model_graph_run(janus_model *m, uint32_t steps) {
+    if (!m) return JANUS_E_INVALID_ARG;
+    if (!m->graph_exec) return fail(m->ctx, JANUS_E_INVALID_ARG, "graph: call janus_model_graph_begin first");
+    for (uint32_t i = 0; i < m->graph_nseq; ++i)
+        if (m->h_pos[i] + steps > m->cfg.max_seq_len)
+            return fail(m->ctx, JANUS_E_KV_OVERFLOW, "graph: steps would exceed max_seq_len");
+    for (uint32_t s = 0; s < steps; ++s) JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(m->graph_exec, m->ctx->stream));
+    for (auto &p : m->h_pos) p += steps;
+    return JANUS_OK;
+}
+
+int janus_model_graph_read_tokens(janus_model *m, uint32_t *h_tokens, uint32_t nseq) {
+    if (!m || !h_tokens || nseq > m->graph_nseq) return JANUS_E_INVALID_ARG;
+    return janus_d2h(m->ctx, h_tokens, m->d_tokens, (size_t)nseq * 4);
+}
+
+}  // extern "C"

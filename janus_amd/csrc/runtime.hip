@@ -1,0 +1,414 @@
+// runtime.hip -- context, buffers, error reporting and weight upload/repack.
+//
+// Stands in for ComputeEngine (crates/janus-engine/src/compute/engine.rs):
+// device init (:27-83), allocate_tensors' per-dtype layout choice
+// (:424-858) and the f16 packing helpers (:112-136).
+#include <cstdio>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "internal.h"
+
+namespace janus {
+
+int fail(janus_ctx *ctx, int code, const std::string &msg) {
+    if (ctx) ctx->last_error = msg;
+    return code;
+}
+
+int hip_fail(janus_ctx *ctx, hipError_t e, const char *what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    int code = (e == hipErrorOutOfMemory) ? JANUS_E_OOM : JANUS_E_HIP;
+    return fail(ctx, code, m);
+}
+
+int ensure_attn_ws(janus_ctx *ctx, size_t bytes) {
+    if (ctx->attn_ws_bytes >= bytes) return JANUS_OK;
+    if (ctx->attn_ws) {
+        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipFree(ctx->attn_ws));
+        ctx->attn_ws = nullptr;
+        ctx->attn_ws_bytes = 0;
+    }
+    size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+    JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->attn_ws, sz));
+    ctx->attn_ws_bytes = sz;
+    return JANUS_OK;
+}
+
+int need_device(janus_ctx *ctx) {
+    if (ctx->device < 0) return fail(ctx, JANUS_E_NO_DEVICE, "validation-only context has no device");
+    return JANUS_OK;
+}
+
+}  // namespace janus
+
+using namespace janus;
+
+namespace {
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) hipSetDevice(dev);
+        else prev = -1;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) hipSetDevice(prev);
+    }
+};
+
+inline uint16_t ftz16(uint16_t h) { return ((h & 0x7c00u) == 0) ? (uint16_t)(h & 0x8000u) : h; }
+
+inline uint16_t f32_to_f16_host(float f) {
+    _Float16 h = (_Float16)f;  // IEEE round-to-nearest-even
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+
+inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// ---- dequantisation kernels (debug/bit-exactness entry) --------------------
+
+__global__ void dequant_q4_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc,
+                                    float *__restrict__ out, size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    float d = h2f(sc[b]);
+    const uint8_t *q = qs + b * 16;
+    for (int j = 0; j < 16; ++j) {
+        out[b * 32 + j] = d * (float)((int)(q[j] & 15) - 8);
+        out[b * 32 + j + 16] = d * (float)((int)(q[j] >> 4) - 8);
+    }
+}
+
+__global__ void dequant_q8_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc,
+                                    float *__restrict__ out, size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    float d = h2f_q8(sc[b]);
+    const int8_t *q = (const int8_t *)(qs + b * 32);
+    for (int j = 0; j < 32; ++j) out[b * 32 + j] = d * (float)q[j];
+}
+
+__device__ __forceinline__ void q4k_scale_min(const uint8_t *s, int j, int &sc, int &mn) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+__global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ blocks, float *__restrict__ out,
+                                    size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t *blk = blocks + b * 144;
+    float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    float dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
+    for (int j = 0; j < 4; ++j) {
+        int sl, ml, sh, mh;
+        q4k_scale_min(blk + 4, 2 * j, sl, ml);
+        q4k_scale_min(blk + 4, 2 * j + 1, sh, mh);
+        float scale_lo = d * (float)sl, min_lo = dmin * (float)ml;
+        float scale_hi = d * (float)sh, min_hi = dmin * (float)mh;
+        for (int t = 0; t < 32; ++t) {
+            uint8_t byte = blk[16 + 32 * j + t];
+            out[b * 256 + 64 * j + t] = scale_lo * (float)(byte & 15) - min_lo;
+            out[b * 256 + 64 * j + 32 + t] = scale_hi * (float)(byte >> 4) - min_hi;
+        }
+    }
+}
+
+__global__ void dequant_f16_kernel(const uint16_t *__restrict__ in, float *__restrict__ out, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = h2f(in[i]);
+}
+
+}  // namespace
+
+extern "C" {
+
+int janus_abi_version(void) { return JANUS_ABI_VERSION; }
+
+const char *janus_status_string(int s) {
+    switch (s) {
+    case JANUS_OK: return "ok";
+    case JANUS_E_INVALID_ARG: return "invalid argument";
+    case JANUS_E_INVALID_DIM: return "invalid dimensions";
+    case JANUS_E_UNSUPPORTED_DTYPE: return "unsupported dtype";
+    case JANUS_E_KV_OVERFLOW: return "kv cache overflow";
+    case JANUS_E_TOKEN_RANGE: return "token id out of range";
+    case JANUS_E_HIP: return "hip error";
+    case JANUS_E_OOM: return "out of device memory";
+    case JANUS_E_NO_DEVICE: return "no device";
+    default: return "unknown status";
+    }
+}
+
+int janus_device_count(int *count) {
+    if (!count) return JANUS_E_INVALID_ARG;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return JANUS_OK;
+}
+
+int janus_create(int hip_device, janus_ctx **out) {
+    if (!out) return JANUS_E_INVALID_ARG;
+    *out = nullptr;
+    if (hip_device == -1) {   // validation-only context: host-side checks, no device work
+        janus_ctx *v = new (std::nothrow) janus_ctx();
+        if (!v) return JANUS_E_OOM;
+        v->device = -1;
+        *out = v;
+        return JANUS_OK;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return JANUS_E_NO_DEVICE;
+    if (hip_device < 0 || hip_device >= n) return JANUS_E_INVALID_ARG;
+    janus_ctx *ctx = new (std::nothrow) janus_ctx();
+    if (!ctx) return JANUS_E_OOM;
+    ctx->device = hip_device;
+    if (hipSetDevice(hip_device) != hipSuccess) {
+        delete ctx;
+        return JANUS_E_HIP;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, hip_device) == hipSuccess) ctx->num_cus = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return JANUS_E_HIP;
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return JANUS_OK;
+}
+
+void janus_destroy(janus_ctx *ctx) {
+    if (!ctx) return;
+    if (ctx->device < 0) {
+        delete ctx;
+        return;
+    }
+    DeviceGuard g(ctx->device);
+    if (ctx->own_stream) hipStreamSynchronize(ctx->own_stream);
+    if (ctx->stream && ctx->stream != ctx->own_stream) hipStreamSynchronize(ctx->stream);
+    if (ctx->attn_ws) hipFree(ctx->attn_ws);
+    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+const char *janus_last_error(const janus_ctx *ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+int janus_set_stream(janus_ctx *ctx, void *s) {
+    if (!ctx) return JANUS_E_INVALID_ARG;
+    if (int e = need_device(ctx)) return e;
+    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    return JANUS_OK;
+}
+
+void *janus_get_stream(janus_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int janus_sync(janus_ctx *ctx) {
+    if (!ctx) return JANUS_E_INVALID_ARG;
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    return JANUS_OK;
+}
+
+int janus_alloc(janus_ctx *ctx, size_t bytes, void **d_ptr) {
+    if (!ctx || !d_ptr || bytes == 0) return fail(ctx, JANUS_E_INVALID_ARG, "janus_alloc: bad argument");
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    JANUS_HIP_CHECK(ctx, hipMalloc(d_ptr, bytes));
+    return JANUS_OK;
+}
+
+int janus_free(janus_ctx *ctx, void *d_ptr) {
+    if (!ctx) return JANUS_E_INVALID_ARG;
+    if (!d_ptr) return JANUS_OK;
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    JANUS_HIP_CHECK(ctx, hipFree(d_ptr));
+    return JANUS_OK;
+}
+
+int janus_h2d(janus_ctx *ctx, void *d, const void *h, size_t bytes) {
+    if (!ctx || (!d && bytes) || (!h && bytes)) return fail(ctx, JANUS_E_INVALID_ARG, "janus_h2d: null pointer");
+    if (!bytes) return JANUS_OK;
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    JANUS_HIP_CHECK(ctx, hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, ctx->stream));
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    return JANUS_OK;
+}
+
+int janus_d2h(janus_ctx *ctx, void *h, const void *d, size_t bytes) {
+    if (!ctx || (!d && bytes) || (!h && bytes)) return fail(ctx, JANUS_E_INVALID_ARG, "janus_d2h: null pointer");
+    if (!bytes) return JANUS_OK;
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    JANUS_HIP_CHECK(ctx, hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    return JANUS_OK;
+}
+
+int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const void *bytes,
+                        size_t nbytes, uint32_t flags, janus_weight **out) {
+    if (!ctx || !out || !bytes) return fail(ctx, JANUS_E_INVALID_ARG, "janus_weight_upload: null argument");
+    *out = nullptr;
+    if (n == 0 || k == 0) return fail(ctx, JANUS_E_INVALID_DIM, "janus_weight_upload: empty tensor");
+    const uint8_t *src = (const uint8_t *)bytes;
+    size_t elems = (size_t)n * k;
+    std::vector<uint8_t> qs;
+    std::vector<uint16_t> sc;
+    bool ftz = (flags & JANUS_WEIGHT_FTZ_F16) != 0;
+    switch (type) {
+    case JANUS_DT_F32: {
+        if (nbytes != elems * 4) return fail(ctx, JANUS_E_INVALID_DIM, "F32 tensor byte size mismatch");
+        qs.resize(elems * 2);
+        uint16_t *dst = (uint16_t *)qs.data();
+        for (size_t i = 0; i < elems; ++i) {
+            float f;
+            std::memcpy(&f, src + 4 * i, 4);
+            uint16_t h = f32_to_f16_host(f);
+            dst[i] = ftz ? ftz16(h) : h;
+        }
+        type = JANUS_DT_F16;
+        break;
+    }
+    case JANUS_DT_F16: {
+        if (nbytes != elems * 2) return fail(ctx, JANUS_E_INVALID_DIM, "F16 tensor byte size mismatch");
+        qs.resize(elems * 2);
+        uint16_t *dst = (uint16_t *)qs.data();
+        for (size_t i = 0; i < elems; ++i) {
+            uint16_t h = rd16(src + 2 * i);
+            dst[i] = ftz ? ftz16(h) : h;
+        }
+        break;
+    }
+    case JANUS_DT_Q4_0:
+    case JANUS_DT_Q8_0: {
+        if (k % 32) return fail(ctx, JANUS_E_INVALID_DIM,
+                                "quantized gemm requires cols to be multiple of 32, got " + std::to_string(k));
+        size_t nblk = elems / 32, bb = (type == JANUS_DT_Q4_0) ? 18 : 34, qb = bb - 2;
+        if (nbytes != nblk * bb) return fail(ctx, JANUS_E_INVALID_DIM, "quantized tensor byte size mismatch");
+        qs.resize(nblk * qb);
+        sc.resize(nblk);
+        for (size_t b = 0; b < nblk; ++b) {
+            sc[b] = rd16(src + b * bb);
+            std::memcpy(qs.data() + b * qb, src + b * bb + 2, qb);
+        }
+        break;
+    }
+    case JANUS_DT_Q4_K: {
+        if (k % 256) return fail(ctx, JANUS_E_INVALID_DIM,
+                                 "Q4_K gemm requires cols to be multiple of 256, got " + std::to_string(k));
+        size_t nblk = elems / 256;
+        if (nbytes != nblk * 144) return fail(ctx, JANUS_E_INVALID_DIM, "Q4_K tensor byte size mismatch");
+        qs.assign(src, src + nbytes);
+        if (ftz)
+            for (size_t b = 0; b < nblk; ++b) {
+                uint8_t *blk = qs.data() + b * 144;
+                for (int o = 0; o < 4; o += 2) {
+                    uint16_t h = ftz16(rd16(blk + o));
+                    blk[o] = (uint8_t)(h & 0xff);
+                    blk[o + 1] = (uint8_t)(h >> 8);
+                }
+            }
+        break;
+    }
+    default:
+        return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "unsupported tensor dtype " + std::to_string(type));
+    }
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    size_t qs_bytes = (qs.size() + 255) & ~(size_t)255;
+    size_t total = qs_bytes + sc.size() * 2 + 256;
+    janus_weight *w = new (std::nothrow) janus_weight();
+    if (!w) return fail(ctx, JANUS_E_OOM, "host allocation failed");
+    hipError_t e = hipMalloc(&w->base, total);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(ctx, e, "hipMalloc(weight)");
+    }
+    w->type = type;
+    w->n = n;
+    w->k = k;
+    w->flags = flags;
+    w->bytes = total;
+    w->qs = (const uint8_t *)w->base;
+    w->sc = sc.empty() ? nullptr : (const uint16_t *)((uint8_t *)w->base + qs_bytes);
+    e = hipMemcpy(w->base, qs.data(), qs.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !sc.empty())
+        e = hipMemcpy((void *)w->sc, sc.data(), sc.size() * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(w->base);
+        delete w;
+        return hip_fail(ctx, e, "hipMemcpy(weight)");
+    }
+    *out = w;
+    return JANUS_OK;
+}
+
+int janus_weight_free(janus_ctx *ctx, janus_weight *w) {
+    if (!w) return JANUS_OK;
+    if (ctx && ctx->device >= 0) {
+        DeviceGuard g(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+    }
+    if (w->base) hipFree(w->base);
+    delete w;
+    return JANUS_OK;
+}
+
+int janus_weight_info(const janus_weight *w, int *type, uint32_t *n, uint32_t *k, size_t *bytes) {
+    if (!w) return JANUS_E_INVALID_ARG;
+    if (type) *type = w->type;
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    if (bytes) *bytes = w->bytes;
+    return JANUS_OK;
+}
+
+int janus_weight_dequant(janus_ctx *ctx, const janus_weight *w, float *d_out) {
+    if (!ctx || !w || !d_out) return fail(ctx, JANUS_E_INVALID_ARG, "janus_weight_dequant: null argument");
+    if (int e = need_device(ctx)) return e;
+    DeviceGuard g(ctx->device);
+    size_t elems = (size_t)w->n * w->k;
+    const int T = 256;
+    switch (w->type) {
+    case JANUS_DT_Q4_0: {
+        size_t nb = elems / 32;
+        dequant_q4_0_kernel<<<(unsigned)((nb + T - 1) / T), T, 0, ctx->stream>>>(w->qs, w->sc, d_out, nb);
+        break;
+    }
+    case JANUS_DT_Q8_0: {
+        size_t nb = elems / 32;
+        dequant_q8_0_kernel<<<(unsigned)((nb + T - 1) / T), T, 0, ctx->stream>>>(w->qs, w->sc, d_out, nb);
+        break;
+    }
+    case JANUS_DT_Q4_K: {
+        size_t nb = elems / 256;
+        dequant_q4_k_kernel<<<(unsigned)((nb + T - 1) / T), T, 0, ctx->stream>>>(w->qs, d_out, nb);
+        break;
+    }
+    case JANUS_DT_F16:
+        dequant_f16_kernel<<<(unsigned)((elems + T - 1) / T), T, 0, ctx->stream>>>((const uint16_t *)w->qs,
+                                                                                   d_out, elems);
+        break;
+    default:
+        return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "dequant: unsupported dtype");
+    }
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+"""Python handle on the C++ decode driver (include/janus_model.h).
+
+Mirrors the reference's Model API shape: construct from a config and GGUF
+tensors (Model::new, model/transformer/constructor.rs:23-437), run
+`forward(token, pos)` (forward.rs:25-119) and `generate` with the reference's
+loop and greedy-sampler semantics (generation.rs:129-323).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import DT_F16, DT_F32, ModelConfig, check
+from .ops import ComputeEngine
+from .synth import ModelSpec
+
+
+class Model:
+    def __init__(self, engine: ComputeEngine, spec: ModelSpec, max_seq_len: int = 256, max_batch: int = 1,
+                 kv_dtype: int = DT_F32, act_dtype: int = DT_F32):
+        self.engine = engine
+        self.lib = engine.lib
+        self.spec = spec
+        cfg = ModelConfig(spec.hidden, spec.heads, spec.kv_heads, spec.head_dim, spec.ffn, spec.vocab,
+                          spec.layers, max_seq_len, max_batch, spec.rms_eps, spec.rope_theta, kv_dtype, act_dtype)
+        self.cfg = cfg
+        h = C.c_void_p()
+        self._check(self.lib.janus_model_create(engine.ctx, C.byref(cfg), C.byref(h)))
+        self.handle = h
+        for t in spec.tensors:
+            buf = np.ascontiguousarray(t.data).view(np.uint8).reshape(-1)
+            self._check(self.lib.janus_model_set_tensor(h, t.name.encode(), t.ggml_type, t.n, t.k,
+                                                        buf.ctypes.data, buf.nbytes))
+        self._check(self.lib.janus_model_validate(h))
+
+    def _check(self, status: int) -> None:
+        check(status, self.engine.ctx)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.janus_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, tokens: Sequence[int], positions: Sequence[int]) -> None:
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        p = np.ascontiguousarray(np.asarray(positions, dtype=np.uint32))
+        self._check(self.lib.janus_model_forward(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+
+    def logits(self, nseq: int = 1) -> np.ndarray:
+        out = np.empty((nseq, self.spec.vocab), dtype=np.float32)
+        self._check(self.lib.janus_model_read_logits(self.handle, out.ctypes.data, nseq))
+        return out
+
+    def logits_ptr(self) -> int:
+        return self.lib.janus_model_logits(self.handle)
+
+    def generate(self, prompt: Sequence[int], max_tokens: int, repetition_penalty: float = 1.15) -> list[int]:
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint32))
+        out = np.zeros(max(1, max_tokens), dtype=np.uint32)
+        n = C.c_uint32()
+        self._check(self.lib.janus_model_generate(self.handle, p.ctypes.data, len(p), max_tokens,
+                                                  repetition_penalty, out.ctypes.data, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def graph_begin(self, tokens: Sequence[int], positions: Sequence[int]) -> None:
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        p = np.ascontiguousarray(np.asarray(positions, dtype=np.uint32))
+        self._check(self.lib.janus_model_graph_begin(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+
+    def graph_run(self, steps: int) -> None:
+        self._check(self.lib.janus_model_graph_run(self.handle, steps))
+
+    def graph_tokens(self, nseq: int) -> list[int]:
+        out = np.zeros(nseq, dtype=np.uint32)
+        self._check(self.lib.janus_model_graph_read_tokens(self.handle, out.ctypes.data, nseq))
+        return out.tolist()
+
+    def kv_cache_ptr(self, which: int) -> int:
+        return self.lib.janus_model_kv_cache(self.handle, which)

@@ -1,0 +1,147 @@
+"""GPU parity of weight upload, dequantisation and the matrix products.
+
+- janus_weight_dequant is bit-exact against the oracle's dequantisation for
+  every format, including subnormal and inf/nan binary16 scales.
+- GEMV outputs match the oracle (the reference's accumulation order) and an
+  f64 product of the dequantised weights within
+  |y - y64| <= 1e-5 * sum_i |w_i x_i|   (fp32 accumulation, any order).
+- Config-2 shapes (Llama-3-8B Q4_0 GEMV, x fp16 N(0,1), fp16 output) are
+  checked against a float64 GPU product of the dequantised weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+from janus_amd import ops, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+GEN = {2: synth.random_q4_0, 8: synth.random_q8_0, 12: synth.random_q4_k}
+
+
+def _weight(engine, ggml_type, n, k, seed, flags=0):
+    rng = np.random.default_rng(seed)
+    if ggml_type in GEN:
+        raw = GEN[ggml_type](rng, n, k)
+    elif ggml_type == 1:
+        raw = synth.f16_bits(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    else:
+        raw = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    return raw, ops.GpuTensor(engine, ggml_type, n, k, raw, flags)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).reshape(-1).view(np.uint32)
+
+
+@pytest.mark.parametrize("ggml_type,flags", [(2, 0), (8, 0), (12, 0), (12, 1), (1, 0), (1, 1), (0, 1)])
+def test_dequant_bit_exact(engine, ggml_type, flags):
+    n, k = 24, 512
+    raw, w = _weight(engine, ggml_type, n, k, 10 + ggml_type)
+    if ggml_type in (2, 8):   # plant subnormal / inf / nan scales
+        bb = 18 if ggml_type == 2 else 34
+        r = raw.reshape(-1, bb)
+        r[:5, :2] = np.array([0x0001, 0x03FF, 0x7C00, 0xFC00, 0x7E01], np.uint16).view(np.uint8).reshape(-1, 2)
+        w = ops.GpuTensor(engine, ggml_type, n, k, raw, flags)
+    if ggml_type == 12:
+        r = raw.reshape(-1, 144)
+        r[0, 0:2] = np.array([0x0005], np.uint16).view(np.uint8)
+        w = ops.GpuTensor(engine, ggml_type, n, k, raw, flags)
+    got = w.dequant().cpu().numpy()
+    want = O.dequant(ggml_type, raw, n, k, ftz=bool(flags))
+    nan = np.isnan(want.reshape(-1))
+    assert np.array_equal(_bits(got)[~nan], _bits(want)[~nan])
+
+
+def _bound(wf, x):
+    return 1e-5 * (np.abs(wf.astype(np.float64)) @ np.abs(x.astype(np.float64))) + 1e-30
+
+
+# the reference decodes F16 weights and Q4_K d/dmin with f16_to_f32_safe
+FTZ = {0: 1, 1: 1, 2: 0, 8: 0, 12: 1}
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 1])
+@pytest.mark.parametrize("n,k", [(1, 256), (7, 256), (64, 256), (130, 512), (256, 4096), (96, 14336)])
+def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
+    raw, w = _weight(engine, ggml_type, n, k, n + k, FTZ[ggml_type])
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    y = torch.empty(n, dtype=torch.float32, device=DEV)
+    ops.gemm_auto(engine, torch.from_numpy(x).to(DEV), w, y, 1, 1, k, n)
+    got = y.cpu().numpy()
+    want = O.gemm_auto(x, ggml_type, raw, n, k)
+    wf = O.dequant(ggml_type, raw, n, k, ftz=bool(FTZ[ggml_type]))
+    y64 = O.gemv_f64(wf, x)
+    b = _bound(wf, x)
+    assert np.all(np.abs(got - y64) <= b)
+    assert np.all(np.abs(got - want) <= 2 * b)
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 1])
+@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096)])
+def test_gemv_f16_activations(engine, ggml_type, n, k):
+    raw, w = _weight(engine, ggml_type, n, k, 3 * n + k, FTZ[ggml_type])
+    rng = np.random.default_rng(n)
+    xh = rng.standard_normal(k).astype(np.float16)
+    y = torch.empty(n, dtype=torch.float16, device=DEV)
+    ops.gemm_auto(engine, torch.from_numpy(xh).to(DEV), w, y, 1, 1, k, n)
+    got = y.float().cpu().numpy()
+    x = xh.astype(np.float32)
+    wf = O.dequant(ggml_type, raw, n, k, ftz=bool(FTZ[ggml_type]))
+    y64 = O.gemv_f64(wf, x)
+    # fp32 accumulation then one binary16 rounding of the output
+    assert np.all(np.abs(got - y64) <= _bound(wf, x) + np.abs(y64) * 2.0 ** -11 + 2.0 ** -24)
+
+
+def test_gemv_f16_odd_k_generic_path(engine):
+    # ffn_down of the tiny model: k = 688 is not a multiple of 32 -> F16 path
+    n, k = 256, 688
+    raw, w = _weight(engine, 0, n, k, 77, flags=1)
+    x = np.random.default_rng(1).standard_normal(k, dtype=np.float32)
+    y = torch.empty(n, dtype=torch.float32, device=DEV)
+    ops.gemm_auto(engine, torch.from_numpy(x).to(DEV), w, y, 1, 1, k, n)
+    want = O.gemm_auto(x, 0, raw, n, k)
+    wf = O.dequant(0, raw, n, k, ftz=True)
+    assert np.all(np.abs(y.cpu().numpy() - want) <= 2 * _bound(wf, x))
+
+
+def test_gemv_residual_epilogue(engine):
+    n, k = 4096, 4096
+    raw, w = _weight(engine, 2, n, k, 5)
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal(k, dtype=np.float32)).to(DEV)
+    r = torch.from_numpy(rng.standard_normal(n, dtype=np.float32)).to(DEV)
+    plain = torch.empty(n, device=DEV)
+    ops.gemm_auto(engine, x, w, plain, 1, 1, k, n)
+    out = r.clone()
+    ops.gemm_residual(engine, x, w, out, out, 1)   # residual aliases the output
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain + r)
+
+
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (4096, 4096)])
+def test_config2_q4_0_gemv_full_shapes(engine, n, k):
+    """Q4_0, x fp16 N(0,1), fp32 accumulate, fp16 output."""
+    rng = np.random.default_rng(2)
+    raw = synth.random_q4_0(rng, n, k)
+    w = ops.GpuTensor(engine, 2, n, k, raw)
+    xh = torch.from_numpy(rng.standard_normal(k).astype(np.float16)).to(DEV)
+    y = torch.empty(n, dtype=torch.float16, device=DEV)
+    ops.gemm_auto(engine, xh, w, y, 1, 1, k, n)
+    wf = w.dequant()
+    ref = (wf.double() @ xh.double()).float()
+    bound = 1e-5 * (wf.abs().double() @ xh.abs().double()).float() + ref.abs() * 2.0 ** -11 + 2.0 ** -24
+    assert bool(((y.float() - ref).abs() <= bound).all())
+    del wf
+
+
+def test_dims_must_match_weight(engine):
+    _, w = _weight(engine, 2, 64, 256, 1)
+    x = torch.zeros(256, device=DEV)
+    y = torch.zeros(64, device=DEV)
+    with pytest.raises(ops.JanusError) as e:
+        ops.gemm_auto(engine, x, w, y, 1, 1, 256, 65)
+    assert e.value.status == 2
