@@ -1,0 +1,225 @@
+"""Decode benchmark: Llama-3-8B-shape Q4_0 greedy decode on one MI355X.
+
+Workload (BASELINE.json metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
+32; GEMV HBM GB/s vs peak"):
+  * value: batch-1 greedy decode tok/s of a random-init Llama-3-8B-architecture
+    model (32 layers, hidden 4096, 32/8 heads, FFN 14336, vocab 128256, RoPE
+    theta 5e5) with Q4_0 block weights, an F16 LM head, an fp16 KV cache and
+    fp16 activations into the products. A 128-token prompt is prefilled, then
+    each timed step is one HIP-graph decode step (embed -> 32 layers -> LM head
+    -> argmax fed back as the next token).
+  * bs32: the ragged continuous-batch step of BASELINE config 5 (32 sequences,
+    fp16 KV contexts uniform in [256, 4096], one forward pass per step).
+  * roofline: the dominant kernel, the Q4_0 GEMV at the 14336x4096 decode shape
+    (config 2: x fp16, fp32 accumulate, fp16 output), timed with HIP events over
+    graph-replayed back-to-back launches rotating through > 256 MB of weight
+    copies so the Infinity Cache cannot serve them.
+  * cpu_baseline: the CPU oracle (a restatement of the reference arithmetic, not
+    the reference itself) on the same model, one thread, a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 & 32; GEMV HBM GB/s vs peak"
+L3 = dict(hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256, layers=32, rope_theta=500000.0)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def llama3_spec(seed: int, layers: int = 32):
+    from janus_amd import synth
+    return synth.make_model(seed, L3["hidden"], L3["heads"], L3["kv_heads"], L3["ffn"], L3["vocab"], layers,
+                            synth.Q4_0, 1e-5, L3["rope_theta"], embed_type=synth.F16, head_type=synth.F16)
+
+
+def decode_bs1(engine, spec, steps: int, warmup: int, prompt_len: int = 128):
+    import torch
+    from janus_amd import _lib
+    from janus_amd.model import Model
+    max_seq = prompt_len + warmup + steps + 8
+    m = Model(engine, spec, max_seq_len=max_seq, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, spec.vocab, prompt_len).tolist()
+    for p, t in enumerate(prompt):           # prefill token by token (generation.rs:161-173)
+        m.forward([t], [p])
+    m.graph_begin([prompt[-1]], [prompt_len])
+    m.graph_run(warmup)
+    engine.sync()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    m.graph_run(steps)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e)
+    toks = m.graph_tokens(1)
+    m.close()
+    return ms, toks
+
+
+def decode_bs32(engine, spec, steps: int, warmup: int):
+    import torch
+    from janus_amd import _lib
+    from janus_amd.model import Model
+    rng = np.random.default_rng(5)
+    lens = rng.integers(256, 4097, 32)
+    max_seq = int(lens.max()) + warmup + steps + 8
+    m = Model(engine, spec, max_seq_len=max_seq, max_batch=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    shape = (spec.layers, 32 * max_seq, spec.kv_heads, spec.head_dim)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    k = torch.randn(shape, device="cuda", dtype=torch.float16, generator=g)
+    v = torch.randn(shape, device="cuda", dtype=torch.float16, generator=g)
+    m.set_kv_cache(k, v)
+    toks = rng.integers(0, spec.vocab, 32).tolist()
+    m.graph_begin(toks, lens.tolist())
+    m.graph_run(warmup)
+    engine.sync()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    m.graph_run(steps)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e)
+    m.close()
+    del k, v
+    return ms, int(lens.sum())
+
+
+def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
+    """HIP-event timing of back-to-back Q4_0 GEMV launches captured in a graph."""
+    import torch
+    from janus_amd import ops, synth
+    rng = np.random.default_rng(2)
+    raw = synth.random_q4_0(rng, n, k)
+    nbytes = raw.nbytes
+    copies = max(2, int(np.ceil(400e6 / nbytes)))
+    ws = [ops.GpuTensor(engine, ops.DT_Q4_0, n, k, raw) for _ in range(copies)]
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float16)).cuda()
+    y = torch.empty(n, dtype=torch.float16, device="cuda")
+    for i in range(copies):
+        ops.gemm_auto(engine, x, ws[i], y, 1, 1, k, n)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        engine.bind_stream(side)
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(launches):
+                ops.gemm_auto(engine, x, ws[i % copies], y, 1, 1, k, n)
+    engine.bind_stream()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(5):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        graph.replay()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e))
+    us = best * 1e3 / launches
+    algo = nbytes + 2 * k + 2 * n     # weights once, x in, y out (fp16)
+    del graph, ws
+    return us, algo, copies
+
+
+def cpu_baseline(spec, tokens: int = 2):
+    """The oracle (CPU restatement of the reference path), single thread, on a
+    bounded sample: `tokens` decode tokens at positions 0.. of the same model."""
+    from oracle import oracle as O
+    m = O.OracleModel(spec, max_seq_len=16, kv_f16=True)
+    t0 = time.perf_counter()
+    tok = 1
+    for p in range(tokens):
+        logits = m.forward(tok, p)
+        tok = O.argmax_last(logits)
+    dt = time.perf_counter() - t0
+    return tokens / dt, dt
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-bs32", action="store_true")
+    ap.add_argument("--layers", type=int, default=32)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
+        return 2
+
+    import torch
+    from janus_amd import _lib, ops
+    if not _lib.LIB_PATH.exists():
+        from janus_amd import build
+        build.build_library()
+    engine = ops.ComputeEngine(0)
+
+    log("roofline: Q4_0 GEMV 14336x4096")
+    us, algo, copies = gemv_roofline(engine)
+    achieved = algo / us / 1e3
+    log(f"  {us:.2f} us/launch, {achieved:.0f} GB/s over {copies} weight copies")
+
+    log("building Llama-3-8B-shape Q4_0 model (random init)")
+    t0 = time.time()
+    spec = llama3_spec(7, args.layers)
+    log(f"  synthesised in {time.time() - t0:.1f} s")
+    ms, toks = decode_bs1(engine, spec, args.steps, args.warmup)
+    tok_s = args.steps / (ms / 1e3)
+    log(f"bs=1: {ms / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+
+    bs32 = None
+    if not args.no_bs32:
+        steps32 = max(5, args.steps // 10)
+        ms32, ctx_sum = decode_bs32(engine, spec, steps32, 3)
+        bs32 = {"tok_s": round(32 * steps32 / (ms32 / 1e3), 1), "ms_per_step": round(ms32 / steps32, 3),
+                "steps": steps32, "ctx_sum": ctx_sum}
+        log(f"bs=32 ragged: {ms32 / steps32:.3f} ms/step, {bs32['tok_s']} tok/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline: oracle, 1 thread, 2 decode tokens")
+        v, dt = cpu_baseline(spec)
+        cpu = {"value": round(v, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"2 decode tokens (positions 0-1) of the same Llama-3-8B-shape Q4_0 model through "
+                         f"the C oracle, single thread, {dt:.1f} s"}
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (random-init weights, seeded prompt)",
+        "config": {"workload": "Llama-3-8B-shape Q4_0 greedy decode, batch 1, 128-token prompt, fp16 KV, "
+                               "F16 LM head, HIP-graph decode step", "layers": args.layers,
+                   "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
+                     "algorithmic_bytes": algo},
+        "bs32": bs32,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    engine.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

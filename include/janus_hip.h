@@ -73,8 +73,9 @@ void janus_destroy(janus_ctx *ctx);
 const char *janus_last_error(const janus_ctx *ctx);
 const char *janus_status_string(int status);
 int janus_abi_version(void);
-/* Run subsequent calls on `hip_stream` (a hipStream_t); NULL restores the
- * context's own stream. */
+/* Run subsequent calls on `hip_stream` (a hipStream_t) exactly as given:
+ * NULL selects the legacy default stream. A new context runs on its own
+ * non-blocking stream, which janus_get_stream returns before any change. */
 int janus_set_stream(janus_ctx *ctx, void *hip_stream);
 void *janus_get_stream(janus_ctx *ctx);
 int janus_sync(janus_ctx *ctx);                      /* device.poll(wait) */

@@ -52,6 +52,12 @@ int janus_model_set_tensor(janus_model *m, const char *name, int ggml_type, uint
 int janus_model_validate(janus_model *m);
 /* KVCache::reset (compute/cache/core.rs). */
 int janus_model_reset(janus_model *m);
+/* Use caller-owned K and V cache buffers (each layers * max_batch * max_seq_len
+ * * kv_heads * head_dim elements of kv_dtype, layout [layer][row][kvh][hd])
+ * instead of the model's own; the model's allocation is released. Lets a
+ * caller place or pre-fill the cache (the reference's caller-owned buffers,
+ * model/transformer/constructor.rs:148-344). */
+int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_each);
 /* One decode step for nseq sequences: sequence s consumes tokens[s] at
  * position positions[s] (its KV rows start at s * max_seq_len). Logits land
  * in janus_model_logits()[s][vocab]. */

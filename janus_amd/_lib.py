@@ -94,6 +94,7 @@ _SIGNATURES = {
     "janus_model_set_tensor": (I32, [P, C.c_char_p, I32, U32, U32, P, SZ]),
     "janus_model_validate": (I32, [P]),
     "janus_model_reset": (I32, [P]),
+    "janus_model_set_kv_cache": (I32, [P, P, P, SZ]),
     "janus_model_forward": (I32, [P, P, P, U32]),
     "janus_model_logits": (P, [P]),
     "janus_model_kv_cache": (P, [P, I32]),

@@ -63,7 +63,8 @@ __global__ __launch_bounds__(THREADS) void attn_partial_kernel(AttnArgs a) {
     __shared__ float comb[PS > 1 ? THREADS * DPT : 1];
 
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const uint32_t len = min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq);
+    // lengths beyond the planned splits (or the capacity) are clamped, never read past
+    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * a.chunk);
     const uint32_t start = split * a.chunk;
     if (start >= len && !(split == 0 && len == 0)) return;   // len 0: split 0 writes zeros
     const uint32_t end = min(len, start + a.chunk);
@@ -184,7 +185,8 @@ __global__ __launch_bounds__(THREADS) void attn_partial_kernel(AttnArgs a) {
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     const uint32_t h = blockIdx.x, b = blockIdx.y;
-    const uint32_t len = min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq);
+    // lengths beyond the planned splits (or the capacity) are clamped, never read past
+    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * a.chunk);
     if (len <= a.chunk) return;   // written directly by the partial kernel
     const uint32_t ns = (len + a.chunk - 1) / a.chunk;
     const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);

@@ -23,9 +23,18 @@
 //  * The R partial sums are reduced across the LPR lanes with a transposed
 //    butterfly (log2 R exchange steps that halve the live values, then a
 //    plain xor butterfly), so the reduction costs O(R + log LPR) shuffles.
+#include <type_traits>
+
 #include "internal.h"
 
 namespace {
+
+#ifndef JANUS_GEMV_WPC
+#define JANUS_GEMV_WPC 16    // most resident wavefronts per CU the register kernel's grid asks for
+#endif
+#ifndef JANUS_GEMV_NT
+#define JANUS_GEMV_NT 1      // stream weights with non-temporal loads
+#endif
 
 constexpr int XB = 32;                 // activation elements per LDS block
 template <typename XT> struct XLayout;
@@ -43,6 +52,28 @@ __device__ __forceinline__ float cvt_b3(uint32_t u) { return (float)(u >> 24); }
 
 __device__ __forceinline__ jh2 as_h2(uint32_t u) { return __builtin_bit_cast(jh2, u); }
 __device__ __forceinline__ float dot2(jh2 a, jh2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// (x0,x1),(x2,x3) -> (x0,x2),(x1,x3): the pair order the nibble unpack produces.
+__device__ __forceinline__ void perm4(uint32_t w01, uint32_t w23, jh2 &even, jh2 &odd) {
+    even = as_h2(__builtin_amdgcn_perm(w23, w01, 0x05040100u));
+    odd = as_h2(__builtin_amdgcn_perm(w23, w01, 0x07060302u));
+}
+
+// 16 halves at p (16-byte aligned) -> 8 permuted pairs, plus their fp32 sum.
+__device__ __forceinline__ float load16h_perm(const _Float16 *p, jh2 *dst) {
+    const uint4 *q = (const uint4 *)p;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint4 t = q[i];
+        perm4(t.x, t.y, dst[4 * i + 0], dst[4 * i + 1]);
+        perm4(t.z, t.w, dst[4 * i + 2], dst[4 * i + 3]);
+        jh2 a = as_h2(t.x), b = as_h2(t.y), c = as_h2(t.z), d = as_h2(t.w);
+        s += ((float)a.x + (float)a.y) + ((float)b.x + (float)b.y) + ((float)c.x + (float)c.y) +
+             ((float)d.x + (float)d.y);
+    }
+    return s;
+}
 
 // ---------------------------------------------------------------------------
 // x staging
@@ -145,6 +176,25 @@ struct FQ4_0 {
         }
         return r;
     }
+    // register-resident x, read straight from global memory
+    __device__ static XF loadx_g(const float *x, int u) {
+        XF r;
+        const jf4 *p = (const jf4 *)(x + (size_t)u * 32);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            r.v[i] = p[i];
+            s += (r.v[i].x + r.v[i].y) + (r.v[i].z + r.v[i].w);
+        }
+        r.s = s;
+        return r;
+    }
+    __device__ static XH loadx_g(const _Float16 *x, int u) {
+        XH r;
+        load16h_perm(x + (size_t)u * 32, r.v);
+        load16h_perm(x + (size_t)u * 32 + 16, r.v + 8);
+        return r;
+    }
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
         const jh2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
@@ -184,6 +234,8 @@ struct FQ8_0 {
     using XH = FQ4_0::XH;
     __device__ static XF loadx(const float *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
     __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
+    __device__ static XF loadx_g(const float *x, int u) { return FQ4_0::loadx_g(x, u); }
+    __device__ static XH loadx_g(const _Float16 *x, int u) { return FQ4_0::loadx_g(x, u); }
     __device__ static float dot(const W &w, const XF &x) {
         const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
         float s0 = 0.0f, s1 = 0.0f;
@@ -264,6 +316,32 @@ struct FQ4_K {
         }
         r.slo = sx16[2 * blo + h];
         r.shi = sx16[2 * bhi + h];
+        r.c = c;
+        return r;
+    }
+    __device__ static XF loadx_g(const float *x, int u) {
+        int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
+        const float *base = x + (size_t)sb * 256 + 64 * j + 16 * h;
+        XF r;
+        float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.lo[i] = ((const jf4 *)base)[i];
+            r.hi[i] = ((const jf4 *)(base + 32))[i];
+            sl += (r.lo[i].x + r.lo[i].y) + (r.lo[i].z + r.lo[i].w);
+            sh += (r.hi[i].x + r.hi[i].y) + (r.hi[i].z + r.hi[i].w);
+        }
+        r.slo = sl;
+        r.shi = sh;
+        r.c = c;
+        return r;
+    }
+    __device__ static XH loadx_g(const _Float16 *x, int u) {
+        int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
+        const _Float16 *base = x + (size_t)sb * 256 + 64 * j + 16 * h;
+        XH r;
+        r.slo = load16h_perm(base, r.lo);
+        r.shi = load16h_perm(base + 32, r.hi);
         r.c = c;
         return r;
     }
@@ -355,6 +433,18 @@ struct FF16 {
     __device__ static XH loadx(const _Float16 *xs, const float *, int u) {
         XH r;
         r.v = *(const uint4 *)(xs + (u >> 2) * XLayout<_Float16>::STRIDE + (u & 3) * 8);
+        return r;
+    }
+    __device__ static XF loadx_g(const float *x, int u) {
+        const jf4 *p = (const jf4 *)(x + (size_t)u * 8);
+        XF r;
+        r.a = p[0];
+        r.b = p[1];
+        return r;
+    }
+    __device__ static XH loadx_g(const _Float16 *x, int u) {
+        XH r;
+        r.v = *(const uint4 *)(x + (size_t)u * 8);
         return r;
     }
     __device__ static float dot(const W &w, const XF &x) {
@@ -472,6 +562,146 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// Cross-lane reduction for a full wavefront per row (LPR = 64), R <= 4 rows:
+// v_permlane32_swap / v_permlane16_swap exchange halves of two row partials
+// at once (the transposed steps), DPP row rotations finish each 16-lane row.
+// On return every lane holds the total of row `ridx`; lanes with
+// lane % (64 / R) == 0 are the writers.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+template <int R>
+__device__ __forceinline__ float reduce_wave_rows(float (&v)[R], int lane, int &ridx) {
+    static_assert(R == 1 || R == 2 || R == 4, "R must be 1, 2 or 4");
+    float s;
+    if (R == 1) {
+        s = swap16_sum(v[0], v[0]);
+        s = swap32_sum(s, s);
+        ridx = 0;
+    } else if (R == 2) {
+        s = swap32_sum(v[0], v[1]);          // lanes < 32: row 0, lanes >= 32: row 1
+        s = swap16_sum(s, s);
+        ridx = lane >> 5;
+    } else {
+        float a = swap32_sum(v[0], v[2]);    // rows 0 | 2
+        float b = swap32_sum(v[1], v[3]);    // rows 1 | 3
+        s = swap16_sum(a, b);                // rows 0,1 | 2,3 by 16-lane row
+        ridx = ((lane >> 5) << 1) | ((lane >> 4) & 1);
+    }
+    s += dpp_f<0x128>(s);   // row_ror:8
+    s += dpp_f<0x124>(s);   // row_ror:4
+    s += dpp_f<0x122>(s);   // row_ror:2
+    s += dpp_f<0x121>(s);   // row_ror:1
+    return s;
+}
+
+// Register-resident variant: each lane keeps x for its units in registers
+// (read once per wavefront from global memory, no LDS, no barriers) and every
+// wavefront walks row groups g, g + W, ... (W = wavefronts in the grid). The
+// steady-state loop is branch-free: the next group's weights are loaded while
+// the current group is reduced, so the loads of one stage stay in flight
+// behind the arithmetic of the other.
+template <class F, typename XT, int BPL, int R, bool FULL>
+__device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const int units = (int)a.units;
+    const uint32_t groups = (a.n + R - 1) / R;
+    using XR = std::conditional_t<sizeof(XT) == 2, typename F::XH, typename F::XF>;
+    using WT = typename F::W;
+
+    int uu[BPL];
+    bool ok[BPL];
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) {
+        const int u = lane + 64 * i;
+        ok[i] = FULL || u < units;
+        uu[i] = ok[i] ? u : units - 1;   // clamped: always a valid address
+    }
+    WT wa[BPL][R], wb[BPL][R];
+    auto load = [&](WT (&w)[BPL][R], uint32_t g) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t row = g * R + r;
+            row = row < a.n ? row : a.n - 1;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) w[i][r] = F::load(a.w, (size_t)row * units + uu[i]);
+        }
+    };
+    const uint32_t mine = (groups - 1 - wave) / nwaves + 1;   // groups this wavefront owns
+    load(wa, wave);
+
+    XR xr[BPL];
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) xr[i] = F::loadx_g((const XT *)a.x, uu[i]);
+
+    // Row written by this lane after the reduction (a static function of the lane).
+    const int my_ridx = R == 1 ? 0 : R == 2 ? (lane >> 5) : (((lane >> 5) << 1) | ((lane >> 4) & 1));
+    const bool writer = (lane & (64 / R - 1)) == 0;
+    // The residual of a group is read before the next group's weights are
+    // requested, so waiting for it never waits for the prefetch.
+    auto load_resid = [&](uint32_t g) -> float {
+        const uint32_t row = g * R + my_ridx;
+        return (a.epi == EPI_RESIDUAL && row < a.n) ? a.resid[row] : 0.0f;
+    };
+    auto consume = [&](WT (&w)[BPL][R], uint32_t g, float resid) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < BPL; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float d = F::dot(w[i][r], xr[i]);
+                acc[r] = ok[i] ? acc[r] + d : acc[r];
+            }
+        int ridx;
+        float s = reduce_wave_rows<R>(acc, lane, ridx);
+        const uint32_t row = g * R + ridx;
+        if (writer && row < a.n) {
+            s += resid;
+            if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
+            else ((float *)a.y)[row] = s;
+        }
+    };
+
+    uint32_t it = 0, g = wave;
+    float ra = load_resid(g), rb;
+    for (; it + 2 < mine; it += 2, g += 2 * nwaves) {
+        rb = load_resid(g + nwaves);
+        load(wb, g + nwaves);
+        consume(wa, g, ra);
+        ra = load_resid(g + 2 * nwaves);
+        load(wa, g + 2 * nwaves);
+        consume(wb, g + nwaves, rb);
+    }
+    if (it + 1 < mine) {
+        rb = load_resid(g + nwaves);
+        load(wb, g + nwaves);
+        consume(wa, g, ra);
+        consume(wb, g + nwaves, rb);
+    } else {
+        consume(wa, g, ra);
+    }
+}
+
+template <class F, typename XT, int BPL, int R>
+__global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (wave >= (a.n + R - 1) / R) return;
+    if (a.units == 64u * BPL) gemv_reg_body<F, XT, BPL, R, true>(a);
+    else gemv_reg_body<F, XT, BPL, R, false>(a);
+}
+
 // Generic fallback for F16 weights whose k is not a multiple of 8: one
 // wavefront per row, scalar loads (the tiny-model ffn_down case, k = 688).
 template <typename XIN>
@@ -530,8 +760,61 @@ int launch_fmt(janus_ctx *ctx, const GemvArgs &a) {
     return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: row too long");
 }
 
+// Persistent grid: as many workgroups as can be resident at once (from the
+// occupancy the compiled kernel allows, capped at JANUS_GEMV_WPC wavefronts
+// per CU); each wavefront then walks several row groups.
+template <class F, typename XT, int BPL, int R>
+int launch_reg(janus_ctx *ctx, const GemvArgs &a) {
+    static int per_cu = 0;
+    if (per_cu == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_reg_kernel<F, XT, BPL, R>, 256, 0) != hipSuccess ||
+            nb < 1)
+            nb = 1;
+        per_cu = nb < JANUS_GEMV_WPC / 4 ? nb : JANUS_GEMV_WPC / 4;
+        if (per_cu < 1) per_cu = 1;
+    }
+    const uint32_t groups = (a.n + R - 1) / R;
+    uint32_t blocks = (groups + 3) / 4;
+    const uint32_t cap = (uint32_t)ctx->num_cus * per_cu;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL((gemv_reg_kernel<F, XT, BPL, R>), dim3(blocks), dim3(256), 0, ctx->stream, a);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// Units per lane = ceil(units / 64); R rows per wavefront step keep at least
+// ~4 KB of weights in flight per stage. x must fit ~128 VGPRs per lane.
+template <class F, typename XT>
+int launch_reg_fmt(janus_ctx *ctx, const GemvArgs &a, bool &done) {
+    constexpr int XREGS = sizeof(std::conditional_t<sizeof(XT) == 2, typename F::XH, typename F::XF>) / 4;
+    const int bpl = (int)((a.units + 63) / 64);
+    done = bpl * XREGS <= 132 && a.units >= 64;
+    if (!done) return JANUS_OK;
+    switch (bpl) {
+    case 1: return launch_reg<F, XT, 1, 4>(ctx, a);
+    case 2: return launch_reg<F, XT, 2, 2>(ctx, a);
+    case 3: return launch_reg<F, XT, 3, 1>(ctx, a);
+    case 4: return launch_reg<F, XT, 4, 1>(ctx, a);
+    case 5: return launch_reg<F, XT, (XREGS * 5 <= 132 ? 5 : 1), 1>(ctx, a);
+    case 6: return launch_reg<F, XT, (XREGS * 6 <= 132 ? 6 : 1), 1>(ctx, a);
+    case 7: return launch_reg<F, XT, (XREGS * 7 <= 132 ? 7 : 1), 1>(ctx, a);
+    case 8: return launch_reg<F, XT, (XREGS * 8 <= 132 ? 8 : 1), 1>(ctx, a);
+    default: break;
+    }
+    if (bpl <= 16 && XREGS * 16 <= 132) return launch_reg<F, XT, (XREGS * 16 <= 132 ? 16 : 1), 1>(ctx, a);
+    if (bpl <= 32 && XREGS * 32 <= 132) return launch_reg<F, XT, (XREGS * 32 <= 132 ? 32 : 1), 1>(ctx, a);
+    done = false;
+    return JANUS_OK;
+}
+
 template <class F>
 int launch_gemv(janus_ctx *ctx, GemvArgs a, int x_dt) {
+    bool done = false;
+    int e;
+    if (x_dt == JANUS_DT_F16) e = launch_reg_fmt<F, _Float16>(ctx, a, done);
+    else e = launch_reg_fmt<F, float>(ctx, a, done);
+    if (done || e) return e;
     if (x_dt == JANUS_DT_F16) return launch_fmt<F, _Float16, _Float16>(ctx, a);
     return launch_fmt<F, float, float>(ctx, a);
 }

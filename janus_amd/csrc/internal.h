@@ -111,8 +111,12 @@ typedef uint32_t ju4 __attribute__((ext_vector_type(4)));
 
 // 128-bit streaming load (non-temporal: weights are read once per launch).
 __device__ __forceinline__ uint4 ld_stream(const void *p) {
+#if !defined(JANUS_GEMV_NT) || JANUS_GEMV_NT
     ju4 v = __builtin_nontemporal_load((const ju4 *)p);
     return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *(const uint4 *)p;
+#endif
 }
 
 // Exact binary16 -> binary32 (subnormals kept). Hardware conversion is exact

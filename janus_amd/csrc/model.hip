@@ -35,6 +35,7 @@ struct janus_model {
     float *gate = nullptr, *up = nullptr, *logits = nullptr;
     void *xn = nullptr, *act = nullptr;   // act_dtype
     void *kcache = nullptr, *vcache = nullptr;
+    bool kv_external = false;
     size_t layer_kv_elems = 0;
     float *rope = nullptr;
     int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_gen = nullptr;
@@ -42,6 +43,7 @@ struct janus_model {
     uint32_t graph_nseq = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    hipStream_t cap_stream = nullptr;
 };
 
 namespace {
@@ -55,11 +57,6 @@ int parse_layer_name(const std::string &name, uint32_t *layer, std::string *rest
     *layer = (uint32_t)std::stoul(name.substr(4, dot - 4));
     *rest = name.substr(dot + 1);
     return 1;
-}
-
-__global__ void lens_from_pos_kernel(const int32_t *pos, int32_t *lens, uint32_t n) {
-    uint32_t i = threadIdx.x;
-    if (i < n) lens[i] = pos[i] + 1;
 }
 
 __global__ void advance_pos_kernel(int32_t *pos, int32_t *lens, uint32_t n) {
@@ -193,6 +190,7 @@ void janus_model_destroy(janus_model *m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
     free_graph(m);
+    if (m->cap_stream) hipStreamDestroy(m->cap_stream);
     for (auto &L : m->layers) {
         for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) janus_weight_free(m->ctx, w);
         hipFree(L.attn_norm);
@@ -202,7 +200,8 @@ void janus_model_destroy(janus_model *m) {
     janus_weight_free(m->ctx, m->lm_head);
     for (void *p : {(void *)m->out_norm, (void *)m->hidden, (void *)m->q, (void *)m->k, (void *)m->v,
                     (void *)m->attn, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
-                    m->act, m->kcache, m->vcache, (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
+                    m->act, m->kv_external ? nullptr : m->kcache, m->kv_external ? nullptr : m->vcache,
+                    (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
                     (void *)m->d_tokens, (void *)m->d_gen})
         if (p) hipFree(p);
     delete m;
@@ -274,6 +273,24 @@ int janus_model_validate(janus_model *m) {
         if (!L.attn_norm || !L.ffn_norm || !L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down)
             return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
     }
+    return JANUS_OK;
+}
+
+int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_each) {
+    if (!m || !d_k || !d_v) return JANUS_E_INVALID_ARG;
+    const size_t need = (size_t)m->cfg.layers * m->layer_kv_elems * kv_elem_bytes(m->cfg.kv_dtype);
+    if (bytes_each < need)
+        return fail(m->ctx, JANUS_E_INVALID_DIM, "set_kv_cache: buffers hold " + std::to_string(bytes_each) +
+                                                     " bytes, need " + std::to_string(need));
+    JANUS_HIP_CHECK(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    free_graph(m);
+    if (!m->kv_external) {
+        hipFree(m->kcache);
+        hipFree(m->vcache);
+    }
+    m->kcache = d_k;
+    m->vcache = d_v;
+    m->kv_external = true;
     return JANUS_OK;
 }
 
@@ -366,15 +383,27 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
     m->h_pos.assign(positions, positions + nseq);
     m->graph_nseq = nseq;
     free_graph(m);
-    JANUS_HIP_CHECK(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    int e = forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
+    // Capture on the model's own stream (the caller's may be the legacy
+    // default stream, which cannot be captured); the graph is launched on the
+    // caller's stream afterwards.
+    if (!m->cap_stream) JANUS_HIP_CHECK(ctx, hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
+    hipStream_t user = ctx->stream;
+    ctx->stream = m->cap_stream;
+    int e = JANUS_OK;
+    hipError_t be = hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal);
+    if (be != hipSuccess) {
+        ctx->stream = user;
+        return hip_fail(ctx, be, "hipStreamBeginCapture");
+    }
+    e = forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
     if (!e) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
     if (!e) {
         hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq);
         if (hipGetLastError() != hipSuccess) e = JANUS_E_HIP;
     }
     hipGraph_t g = nullptr;
-    hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
+    hipError_t ce = hipStreamEndCapture(m->cap_stream, &g);
+    ctx->stream = user;
     if (e) {
         if (g) hipGraphDestroy(g);
         return e;

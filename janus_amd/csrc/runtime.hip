@@ -208,7 +208,7 @@ const char *janus_last_error(const janus_ctx *ctx) { return ctx ? ctx->last_erro
 int janus_set_stream(janus_ctx *ctx, void *s) {
     if (!ctx) return JANUS_E_INVALID_ARG;
     if (int e = need_device(ctx)) return e;
-    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    ctx->stream = (hipStream_t)s;   // NULL is the device's legacy default stream
     return JANUS_OK;
 }
 

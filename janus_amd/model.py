@@ -84,5 +84,11 @@ class Model:
         self._check(self.lib.janus_model_graph_read_tokens(self.handle, out.ctypes.data, nseq))
         return out.tolist()
 
+    def set_kv_cache(self, k, v) -> None:
+        """Use caller-owned cache tensors [layers, max_batch * max_seq_len, kv_heads, head_dim]."""
+        self._k_ext, self._v_ext = k, v   # keep them alive
+        self._check(self.lib.janus_model_set_kv_cache(self.handle, k.data_ptr(), v.data_ptr(),
+                                                      k.numel() * k.element_size()))
+
     def kv_cache_ptr(self, which: int) -> int:
         return self.lib.janus_model_kv_cache(self.handle, which)

@@ -39,7 +39,7 @@ def _bits(a):
 @pytest.mark.parametrize("ggml_type,flags", [(2, 0), (8, 0), (12, 0), (12, 1), (1, 0), (1, 1), (0, 1)])
 def test_dequant_bit_exact(engine, ggml_type, flags):
     n, k = 24, 512
-    raw, w = _weight(engine, ggml_type, n, k, 10 + ggml_type)
+    raw, w = _weight(engine, ggml_type, n, k, 10 + ggml_type, flags)
     if ggml_type in (2, 8):   # plant subnormal / inf / nan scales
         bb = 18 if ggml_type == 2 else 34
         r = raw.reshape(-1, bb)
