@@ -492,17 +492,25 @@ __device__ __forceinline__ float reduce_rows(float (&v)[R], int li, int &ridx) {
     return s;
 }
 
-enum { EPI_STORE = 0, EPI_RESIDUAL = 1 };
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3 };
 
 struct GemvArgs {
     WPtr w;
     const void *x;       // activation [k]
-    void *y;             // output [n]
+    void *y;             // output [n] (EPI_SWIGLU: [n / 2])
     const float *resid;  // residual [n] (EPI_RESIDUAL)
     uint32_t n, k;
     uint32_t units;      // units per row
     int out_f16;
     int epi;
+    // EPI_QKV_ROPE: row pairs are (i, i + hd/2) of a q head, then of a k head,
+    // then consecutive v elements; q is rotated into y (f32), k is rotated and
+    // v copied into the cache row of position d_pos[0].
+    void *kc, *vc;
+    const float *rope;
+    const int32_t *d_pos;
+    uint32_t q_pairs, k_pairs, half_hd, kv_row;
+    int kv_f16;
 };
 
 template <class F, typename XIN, typename XT, int LPR, int R, int BPL_MAX>
@@ -647,13 +655,22 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
     // Row written by this lane after the reduction (a static function of the lane).
     const int my_ridx = R == 1 ? 0 : R == 2 ? (lane >> 5) : (((lane >> 5) << 1) | ((lane >> 4) & 1));
     const bool writer = (lane & (64 / R - 1)) == 0;
-    // The residual of a group is read before the next group's weights are
-    // requested, so waiting for it never waits for the prefetch.
-    auto load_resid = [&](uint32_t g) -> float {
-        const uint32_t row = g * R + my_ridx;
-        return (a.epi == EPI_RESIDUAL && row < a.n) ? a.resid[row] : 0.0f;
+    const uint32_t pos = (a.epi == EPI_QKV_ROPE) ? (uint32_t)a.d_pos[0] : 0u;
+    // Per-group side data (the residual, or the RoPE cos/sin pair) is read
+    // before the next group's weights are requested, so waiting for it never
+    // waits for the prefetch.
+    auto load_side = [&](uint32_t g) -> float2 {
+        if (a.epi == EPI_RESIDUAL) {
+            const uint32_t row = g * R + my_ridx;
+            return make_float2(row < a.n ? a.resid[row] : 0.0f, 0.0f);
+        }
+        if (a.epi == EPI_QKV_ROPE && g < a.q_pairs + a.k_pairs) {
+            const uint32_t i = (g < a.q_pairs ? g : g - a.q_pairs) % a.half_hd;
+            return *(const float2 *)(a.rope + 2 * ((size_t)pos * a.half_hd + i));
+        }
+        return make_float2(0.0f, 0.0f);
     };
-    auto consume = [&](WT (&w)[BPL][R], uint32_t g, float resid) {
+    auto consume = [&](WT (&w)[BPL][R], uint32_t g, float2 side) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -666,26 +683,69 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
             }
         int ridx;
         float s = reduce_wave_rows<R>(acc, lane, ridx);
+        if (R == 2 && a.epi >= EPI_QKV_ROPE) {
+            // both row totals in every lane: lanes < 32 hold row 0, lanes >= 32 row 1
+            auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+            const float r0 = __uint_as_float(p[0]), r1 = __uint_as_float(p[1]);
+            if (lane == 0 && 2 * g < a.n) {
+                if (a.epi == EPI_SWIGLU) {
+                    // rows (2g, 2g + 1) = (gate_g, up_g): act_g = silu(gate) * up
+                    const float v = r0 * (1.0f / (1.0f + expf(-r0))) * r1;
+                    if (a.out_f16) ((uint16_t *)a.y)[g] = f2h_bits(v);
+                    else ((float *)a.y)[g] = v;
+                } else if (g < a.q_pairs + a.k_pairs) {
+                    // rope.wgsl:71-72 on the pair (x0, x1) = (r0, r1)
+                    const float y0 = r0 * side.x - r1 * side.y;
+                    const float y1 = r0 * side.y + r1 * side.x;
+                    if (g < a.q_pairs) {
+                        const uint32_t h = g / a.half_hd, i = g % a.half_hd;
+                        float *q = (float *)a.y + (size_t)h * 2 * a.half_hd + i;
+                        q[0] = y0;
+                        q[a.half_hd] = y1;
+                    } else {
+                        const uint32_t gk = g - a.q_pairs, h = gk / a.half_hd, i = gk % a.half_hd;
+                        const size_t at = (size_t)pos * a.kv_row + (size_t)h * 2 * a.half_hd + i;
+                        if (a.kv_f16) {
+                            ((_Float16 *)a.kc)[at] = (_Float16)y0;
+                            ((_Float16 *)a.kc)[at + a.half_hd] = (_Float16)y1;
+                        } else {
+                            ((float *)a.kc)[at] = y0;
+                            ((float *)a.kc)[at + a.half_hd] = y1;
+                        }
+                    }
+                } else {
+                    const size_t at = (size_t)pos * a.kv_row + 2 * (size_t)(g - a.q_pairs - a.k_pairs);
+                    if (a.kv_f16) {
+                        ((_Float16 *)a.vc)[at] = (_Float16)r0;
+                        ((_Float16 *)a.vc)[at + 1] = (_Float16)r1;
+                    } else {
+                        ((float *)a.vc)[at] = r0;
+                        ((float *)a.vc)[at + 1] = r1;
+                    }
+                }
+            }
+            return;
+        }
         const uint32_t row = g * R + ridx;
         if (writer && row < a.n) {
-            s += resid;
+            s += side.x;
             if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
             else ((float *)a.y)[row] = s;
         }
     };
 
     uint32_t it = 0, g = wave;
-    float ra = load_resid(g), rb;
+    float2 ra = load_side(g), rb;
     for (; it + 2 < mine; it += 2, g += 2 * nwaves) {
-        rb = load_resid(g + nwaves);
+        rb = load_side(g + nwaves);
         load(wb, g + nwaves);
         consume(wa, g, ra);
-        ra = load_resid(g + 2 * nwaves);
+        ra = load_side(g + 2 * nwaves);
         load(wa, g + 2 * nwaves);
         consume(wb, g + nwaves, rb);
     }
     if (it + 1 < mine) {
-        rb = load_resid(g + nwaves);
+        rb = load_side(g + nwaves);
         load(wb, g + nwaves);
         consume(wa, g, ra);
         consume(wb, g + nwaves, rb);
@@ -819,13 +879,66 @@ int launch_gemv(janus_ctx *ctx, GemvArgs a, int x_dt) {
     return launch_fmt<F, float, float>(ctx, a);
 }
 
+// Paired-row products (fused QKV + RoPE + KV append, fused gate/up + SwiGLU):
+// the register kernel with exactly two rows per wavefront step.
+template <class F, typename XT>
+int launch_pair_fmt(janus_ctx *ctx, const GemvArgs &a) {
+    switch ((a.units + 63) / 64) {
+    case 1: return launch_reg<F, XT, 1, 2>(ctx, a);
+    case 2: return launch_reg<F, XT, 2, 2>(ctx, a);
+    case 3: return launch_reg<F, XT, 3, 2>(ctx, a);
+    case 4: return launch_reg<F, XT, 4, 2>(ctx, a);
+    case 5: return launch_reg<F, XT, 5, 2>(ctx, a);
+    case 6: return launch_reg<F, XT, 6, 2>(ctx, a);
+    case 7: return launch_reg<F, XT, 7, 2>(ctx, a);
+    case 8: return launch_reg<F, XT, 8, 2>(ctx, a);
+    default: return janus::fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: row too long");
+    }
+}
+
 }  // namespace
 
 namespace janus {
 
+int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
+                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
+                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row) {
+    GemvArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.w.qs = w->qs;
+    a.w.sc = w->sc;
+    a.x = x;
+    a.y = y;
+    a.n = w->n;
+    a.k = w->k;
+    a.out_f16 = y_f16;
+    a.epi = epi == 0 ? EPI_QKV_ROPE : EPI_SWIGLU;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_f16 = kv_f16;
+    a.rope = rope;
+    a.d_pos = d_pos;
+    a.q_pairs = q_pairs;
+    a.k_pairs = k_pairs;
+    a.half_hd = half_hd;
+    a.kv_row = kv_row;
+    if (w->n % 2) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: odd row count");
+    switch (w->type) {
+    case JANUS_DT_Q4_0: a.units = w->k / 32; return launch_pair_fmt<FQ4_0, _Float16>(ctx, a);
+    case JANUS_DT_Q8_0: a.units = w->k / 32; return launch_pair_fmt<FQ8_0, _Float16>(ctx, a);
+    case JANUS_DT_Q4_K: a.units = w->k / 32; return launch_pair_fmt<FQ4_K, _Float16>(ctx, a);
+    case JANUS_DT_F16:
+        if (w->k % 8) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: F16 rows need k % 8 == 0");
+        a.units = w->k / 8;
+        return launch_pair_fmt<FF16, _Float16>(ctx, a);
+    default: return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "paired gemv: unsupported weight type");
+    }
+}
+
 int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
                   const float *residual) {
     GemvArgs a;
+    std::memset(&a, 0, sizeof(a));
     a.w.qs = w->qs;
     a.w.sc = w->sc;
     a.x = x;

@@ -12,10 +12,55 @@ namespace janus {
 // ---- RMSNorm: one workgroup per row ---------------------------------------
 // y = (x / sqrt(sum(x^2)/H + eps)) * gamma  -- division by the root, as the
 // reference writes it (activations.wgsl:114,128).
-template <bool OUT_F16>
+// Rows of up to 256 * 4 * NV elements are held in registers: every thread
+// issues all of its 16-byte loads at once, so the kernel costs one memory
+// round trip instead of one per strided iteration.
+template <bool OUT_F16, int NV>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ in, void *__restrict__ out,
                                                       const float *__restrict__ gamma, uint32_t hidden,
                                                       float eps) {
+    __shared__ float red[4];
+    const float *x = in + (size_t)blockIdx.x * hidden;
+    const bool vec = (hidden & 3) == 0;
+    float v[NV][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = 4 * (threadIdx.x + 256u * j);
+        if (vec && i < hidden) {
+            jf4 t = *(const jf4 *)(x + i);
+            v[j][0] = t.x; v[j][1] = t.y; v[j][2] = t.z; v[j][3] = t.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[j][c] = (i + c < hidden) ? x[i + c] : 0.0f;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s = fmaf(v[j][c], v[j][c], s);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(tot / (float)hidden + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = 4 * (threadIdx.x + 256u * j);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (i + c < hidden) {
+                float r = (v[j][c] / rms) * gamma[i + c];
+                if (OUT_F16) ((uint16_t *)out)[(size_t)blockIdx.x * hidden + i + c] = f2h_bits(r);
+                else ((float *)out)[(size_t)blockIdx.x * hidden + i + c] = r;
+            }
+        }
+    }
+}
+
+// Rows too long for registers: strided loops.
+template <bool OUT_F16>
+__global__ __launch_bounds__(256) void rmsnorm_long_kernel(const float *__restrict__ in, void *__restrict__ out,
+                                                           const float *__restrict__ gamma, uint32_t hidden,
+                                                           float eps) {
     __shared__ float red[4];
     const float *x = in + (size_t)blockIdx.x * hidden;
     float s = 0.0f;
@@ -23,9 +68,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
-    float tot = 0.0f;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
-    const float rms = sqrtf(tot / (float)hidden + eps);
+    const float rms = sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden + eps);
     for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
         float v = (x[i] / rms) * gamma[i];
         if (OUT_F16) ((uint16_t *)out)[(size_t)blockIdx.x * hidden + i] = f2h_bits(v);
@@ -33,12 +76,19 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     }
 }
 
+template <bool H>
+static void rmsnorm_dispatch(janus_ctx *ctx, const float *in, void *out, const float *gamma, uint32_t batch,
+                             uint32_t hidden, float eps) {
+    if (hidden <= 1024) hipLaunchKernelGGL((rmsnorm_kernel<H, 1>), dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    else if (hidden <= 4096) hipLaunchKernelGGL((rmsnorm_kernel<H, 4>), dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    else if (hidden <= 8192) hipLaunchKernelGGL((rmsnorm_kernel<H, 8>), dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    else hipLaunchKernelGGL((rmsnorm_long_kernel<H>), dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+}
+
 int rmsnorm_launch(janus_ctx *ctx, const float *in, void *out, int out_dt, const float *gamma,
                    uint32_t batch, uint32_t hidden, float eps) {
-    if (out_dt == JANUS_DT_F16)
-        hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
-    else
-        hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(batch), dim3(256), 0, ctx->stream, in, out, gamma, hidden, eps);
+    if (out_dt == JANUS_DT_F16) rmsnorm_dispatch<true>(ctx, in, out, gamma, batch, hidden, eps);
+    else rmsnorm_dispatch<false>(ctx, in, out, gamma, batch, hidden, eps);
     JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
 }

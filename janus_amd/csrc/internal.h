@@ -69,6 +69,16 @@ int need_device(janus_ctx *ctx);
 // M = 1 product (gemv.hip). residual may be null; when set, y must be F32.
 int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
                   const float *residual);
+// Paired-row M = 1 products with x in f16: epi 0 = fused QKV with RoPE and KV
+// append (q rotated into y, f32), epi 1 = fused gate/up with SwiGLU into y.
+int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
+                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
+                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row);
+// Row layout of an uploaded weight (bytes of quants, binary16 scales per row).
+size_t weight_qs_row_bytes(int type, uint32_t k);
+size_t weight_sc_row_elems(int type, uint32_t k);
+// Device allocation of an empty weight of the given type and shape.
+int weight_alloc(janus_ctx *ctx, int type, uint32_t n, uint32_t k, uint32_t flags, janus_weight **out);
 // rows >= 1 product (small-M MFMA GEMM for rows > 1).
 int gemm_dispatch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w, void *c,
                   int c_dt, uint32_t rows, const float *residual);

@@ -26,7 +26,11 @@ struct janus_model {
         float *attn_norm = nullptr, *ffn_norm = nullptr;
         janus_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
         janus_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+        // fused copies for the single-sequence path (built by ensure_fused)
+        janus_weight *qkv = nullptr;   // rows: q RoPE pairs, k RoPE pairs, v
+        janus_weight *gu = nullptr;    // rows: gate_0, up_0, gate_1, up_1, ...
     };
+    bool fused_ready = false;
     std::vector<Layer> layers;
     janus_weight *tok_embd = nullptr, *lm_head = nullptr;
     float *out_norm = nullptr;
@@ -104,6 +108,102 @@ int forward_rows(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, ui
     // final norm + LM head (forward.rs:87-111)
     if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, c.act_dtype, m->out_norm, nseq, c.hidden, c.rms_eps))) return e;
     return gemm_dispatch(ctx, m->xn, c.act_dtype, m->lm_head, m->logits, JANUS_DT_F32, nseq, nullptr);
+}
+
+// Copies `height` rows of a weight (quants and scales) from src rows
+// [s0, s0 + height) to dst rows d0, d0 + dstep, ...
+int copy_rows(janus_ctx *ctx, janus_weight *dst, uint32_t d0, uint32_t dstep, const janus_weight *src, uint32_t s0,
+              uint32_t height) {
+    const size_t qb = weight_qs_row_bytes(src->type, src->k), sb = weight_sc_row_elems(src->type, src->k) * 2;
+    JANUS_HIP_CHECK(ctx, hipMemcpy2DAsync((uint8_t *)dst->qs + (size_t)d0 * qb, dstep * qb, src->qs + (size_t)s0 * qb,
+                                          qb, qb, height, hipMemcpyDeviceToDevice, ctx->stream));
+    if (sb)
+        JANUS_HIP_CHECK(ctx, hipMemcpy2DAsync((uint8_t *)dst->sc + (size_t)d0 * sb, dstep * sb,
+                                              (const uint8_t *)src->sc + (size_t)s0 * sb, sb, sb, height,
+                                              hipMemcpyDeviceToDevice, ctx->stream));
+    return JANUS_OK;
+}
+
+// Builds the fused QKV and gate/up weights of every layer once all tensors
+// are present. QKV rows are ordered so each consecutive pair is a RoPE pair
+// (i, i + hd/2) of one head (q heads, then k heads) followed by v in order;
+// gate/up rows alternate gate_j, up_j. Layers whose tensors differ in type
+// keep the unfused path.
+int ensure_fused(janus_model *m) {
+    if (m->fused_ready) return JANUS_OK;
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const uint32_t hd = c.head_dim, half = hd / 2, kvd = c.kv_heads * hd;
+    for (auto &L : m->layers) {
+        const janus_weight *q = L.q, *k = L.k, *v = L.v;
+        bool same = q->type == k->type && q->type == v->type && q->flags == k->flags && q->flags == v->flags &&
+                    (q->type != JANUS_DT_F16 || q->k % 8 == 0);
+        if (same && !L.qkv) {
+            janus_weight *w = nullptr;
+            if (int e = weight_alloc(ctx, q->type, c.hidden + 2 * kvd, c.hidden, q->flags, &w)) return e;
+            for (uint32_t h = 0; h < c.heads; ++h) {
+                if (int e = copy_rows(ctx, w, h * hd, 2, q, h * hd, half)) return e;
+                if (int e = copy_rows(ctx, w, h * hd + 1, 2, q, h * hd + half, half)) return e;
+            }
+            for (uint32_t h = 0; h < c.kv_heads; ++h) {
+                if (int e = copy_rows(ctx, w, c.hidden + h * hd, 2, k, h * hd, half)) return e;
+                if (int e = copy_rows(ctx, w, c.hidden + h * hd + 1, 2, k, h * hd + half, half)) return e;
+            }
+            if (int e = copy_rows(ctx, w, c.hidden + kvd, 1, v, 0, kvd)) return e;
+            L.qkv = w;
+        }
+        const janus_weight *g = L.gate, *u = L.up;
+        same = g->type == u->type && g->flags == u->flags && (g->type != JANUS_DT_F16 || g->k % 8 == 0);
+        if (same && !L.gu) {
+            janus_weight *w = nullptr;
+            if (int e = weight_alloc(ctx, g->type, 2 * c.ffn, c.hidden, g->flags, &w)) return e;
+            if (int e = copy_rows(ctx, w, 0, 2, g, 0, c.ffn)) return e;
+            if (int e = copy_rows(ctx, w, 1, 2, u, 0, c.ffn)) return e;
+            L.gu = w;
+        }
+    }
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    m->fused_ready = true;
+    return JANUS_OK;
+}
+
+// Single-sequence step over the fused weights (f16 activations): per layer
+// rmsnorm, QKV+RoPE+KV append, attention, o-proj+residual, rmsnorm,
+// gate/up+SwiGLU, down-proj+residual.
+int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t max_len) {
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const uint32_t kvd = c.kv_heads * c.head_dim, half = c.head_dim / 2;
+    const int kv16 = c.kv_dtype == JANUS_DT_F16;
+    int e;
+    if ((e = embed_launch(ctx, m->tok_embd, h_ids, d_ids, 1, m->hidden))) return e;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const janus_model::Layer &L = m->layers[l];
+        void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, L.attn_norm, 1, c.hidden, c.rms_eps))) return e;
+        if ((e = gemv_pair_dispatch(ctx, m->xn, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, c.heads * half,
+                                    c.kv_heads * half, half, kvd)))
+            return e;
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn, 1, c.heads, c.kv_heads, c.head_dim, 0,
+                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim))))
+            return e;
+        if ((e = gemm_dispatch(ctx, m->attn, JANUS_DT_F32, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
+        if ((e = rmsnorm_launch(ctx, m->h1, m->xn, JANUS_DT_F16, L.ffn_norm, 1, c.hidden, c.rms_eps))) return e;
+        if ((e = gemv_pair_dispatch(ctx, m->xn, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0,
+                                    0)))
+            return e;
+        if ((e = gemm_dispatch(ctx, m->act, JANUS_DT_F16, L.down, m->hidden, JANUS_DT_F32, 1, m->h1))) return e;
+    }
+    if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, m->out_norm, 1, c.hidden, c.rms_eps))) return e;
+    return gemm_dispatch(ctx, m->xn, JANUS_DT_F16, m->lm_head, m->logits, JANUS_DT_F32, 1, nullptr);
+}
+
+bool use_fused1(const janus_model *m, uint32_t nseq) {
+    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready) return false;
+    for (const auto &L : m->layers)
+        if (!L.qkv || !L.gu) return false;
+    return true;
 }
 
 struct Positions {
@@ -192,7 +292,7 @@ void janus_model_destroy(janus_model *m) {
     free_graph(m);
     if (m->cap_stream) hipStreamDestroy(m->cap_stream);
     for (auto &L : m->layers) {
-        for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) janus_weight_free(m->ctx, w);
+        for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down, L.qkv, L.gu}) janus_weight_free(m->ctx, w);
         hipFree(L.attn_norm);
         hipFree(L.ffn_norm);
     }
@@ -235,6 +335,12 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
         return JANUS_OK;
     };
     free_graph(m);
+    m->fused_ready = false;
+    for (auto &L : m->layers) {
+        janus_weight_free(ctx, L.qkv);
+        janus_weight_free(ctx, L.gu);
+        L.qkv = L.gu = nullptr;
+    }
     if (name == "token_embd.weight") {
         if (type != JANUS_DT_F32 && type != JANUS_DT_F16)
             return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "token_embd.weight must be F32 or F16");
@@ -273,6 +379,7 @@ int janus_model_validate(janus_model *m) {
         if (!L.attn_norm || !L.ffn_norm || !L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down)
             return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
     }
+    if (m->cfg.act_dtype == JANUS_DT_F16) return ensure_fused(m);
     return JANUS_OK;
 }
 
@@ -316,6 +423,7 @@ int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *
         max_len = positions[i] + 1 > max_len ? positions[i] + 1 : max_len;
     }
     if (int e = upload_positions(m, positions, nseq)) return e;
+    if (use_fused1(m, nseq)) return forward_fused1(m, tokens, nullptr, max_len);
     return forward_rows(m, tokens, nullptr, nseq, max_len);
 }
 
@@ -395,7 +503,8 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
         ctx->stream = user;
         return hip_fail(ctx, be, "hipStreamBeginCapture");
     }
-    e = forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
+    e = use_fused1(m, nseq) ? forward_fused1(m, nullptr, m->d_tokens, m->cfg.max_seq_len)
+                            : forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
     if (!e) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
     if (!e) {
         hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq);

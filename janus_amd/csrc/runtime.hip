@@ -42,6 +42,43 @@ int need_device(janus_ctx *ctx) {
     return JANUS_OK;
 }
 
+size_t weight_qs_row_bytes(int type, uint32_t k) {
+    switch (type) {
+    case JANUS_DT_Q4_0: return (size_t)k / 32 * 16;
+    case JANUS_DT_Q8_0: return (size_t)k / 32 * 32;
+    case JANUS_DT_Q4_K: return (size_t)k / 256 * 144;
+    case JANUS_DT_F16: return (size_t)k * 2;
+    default: return 0;
+    }
+}
+
+size_t weight_sc_row_elems(int type, uint32_t k) {
+    return (type == JANUS_DT_Q4_0 || type == JANUS_DT_Q8_0) ? k / 32 : 0;
+}
+
+int weight_alloc(janus_ctx *ctx, int type, uint32_t n, uint32_t k, uint32_t flags, janus_weight **out) {
+    const size_t qs_used = weight_qs_row_bytes(type, k) * n;
+    const size_t sc_used = weight_sc_row_elems(type, k) * n * 2;
+    const size_t qs_bytes = (qs_used + 255) & ~(size_t)255;
+    const size_t total = qs_bytes + sc_used + 256;
+    janus_weight *w = new (std::nothrow) janus_weight();
+    if (!w) return fail(ctx, JANUS_E_OOM, "host allocation failed");
+    hipError_t e = hipMalloc(&w->base, total);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(ctx, e, "hipMalloc(weight)");
+    }
+    w->type = type;
+    w->n = n;
+    w->k = k;
+    w->flags = flags;
+    w->bytes = total;
+    w->qs = (const uint8_t *)w->base;
+    w->sc = sc_used ? (const uint16_t *)((uint8_t *)w->base + qs_bytes) : nullptr;
+    *out = w;
+    return JANUS_OK;
+}
+
 }  // namespace janus
 
 using namespace janus;
@@ -330,23 +367,9 @@ int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const 
     }
     if (int e = need_device(ctx)) return e;
     DeviceGuard g(ctx->device);
-    size_t qs_bytes = (qs.size() + 255) & ~(size_t)255;
-    size_t total = qs_bytes + sc.size() * 2 + 256;
-    janus_weight *w = new (std::nothrow) janus_weight();
-    if (!w) return fail(ctx, JANUS_E_OOM, "host allocation failed");
-    hipError_t e = hipMalloc(&w->base, total);
-    if (e != hipSuccess) {
-        delete w;
-        return hip_fail(ctx, e, "hipMalloc(weight)");
-    }
-    w->type = type;
-    w->n = n;
-    w->k = k;
-    w->flags = flags;
-    w->bytes = total;
-    w->qs = (const uint8_t *)w->base;
-    w->sc = sc.empty() ? nullptr : (const uint16_t *)((uint8_t *)w->base + qs_bytes);
-    e = hipMemcpy(w->base, qs.data(), qs.size(), hipMemcpyHostToDevice);
+    janus_weight *w = nullptr;
+    if (int st = weight_alloc(ctx, type, n, k, flags, &w)) return st;
+    hipError_t e = hipMemcpy(w->base, qs.data(), qs.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess && !sc.empty())
         e = hipMemcpy((void *)w->sc, sc.data(), sc.size() * 2, hipMemcpyHostToDevice);
     if (e != hipSuccess) {

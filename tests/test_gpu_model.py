@@ -115,3 +115,59 @@ def test_ragged_batch_equals_single_sequences(engine, spec):
     for s in range(4):
         assert _rel_err(out[s], singles[s]) <= 1e-5
     mb.close()
+
+
+def _mini_llama3(seed=11, qtype=synth.Q4_0):
+    """A 2-layer Llama-3-shaped model (head_dim 128, GQA 4:1, theta 5e5) small
+    enough for the oracle: exercises the fused single-sequence path."""
+    return synth.make_model(seed, 512, 4, 1, 1024, 1000, 2, qtype, 1e-5, 500000.0,
+                            embed_type=synth.F16, head_type=synth.F16)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q8_0, synth.Q4_K])
+@pytest.mark.parametrize("kv_dtype", [_lib.DT_F16, _lib.DT_F32])
+def test_fused_f16_activation_path_matches_oracle(engine, qtype, kv_dtype):
+    spec = _mini_llama3(qtype=qtype)
+    prompt = _prompt(5, 24, spec.vocab)
+    ref = O.OracleModel(spec, 64, kv_f16=(kv_dtype == _lib.DT_F16))
+    m = Model(engine, spec, max_seq_len=64, kv_dtype=kv_dtype, act_dtype=_lib.DT_F16)
+    worst = 0.0
+    for p, t in enumerate(prompt):
+        want = ref.forward(t, p)
+        m.forward([t], [p])
+        worst = max(worst, _rel_err(m.logits()[0], want))
+    assert worst <= REL, worst
+    m.close()
+
+
+def test_fused_path_config1_greedy_tokens(engine, spec):
+    prompt = _prompt()
+    ref_tokens = O.OracleModel(spec, 64).generate(prompt, 16)
+    m = Model(engine, spec, max_seq_len=64, act_dtype=_lib.DT_F16)
+    assert m.generate(prompt, 16) == ref_tokens
+    m.close()
+
+
+def test_fused_graph_matches_fused_eager(engine):
+    spec = _mini_llama3(13)
+    prompt = _prompt(8, 10, spec.vocab)
+    outs = []
+    for use_graph in (False, True):
+        m = Model(engine, spec, max_seq_len=64, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for p, t in enumerate(prompt):
+            m.forward([t], [p])
+        toks, last, pos = [], prompt[-1], len(prompt)
+        if use_graph:
+            m.graph_begin([last], [pos])
+            for _ in range(12):
+                m.graph_run(1)
+                toks.append(m.graph_tokens(1)[0])
+        else:
+            for _ in range(12):
+                m.forward([last], [pos])
+                last = O.argmax_last(m.logits()[0])
+                toks.append(last)
+                pos += 1
+        outs.append(toks)
+        m.close()
+    assert outs[0] == outs[1]
