@@ -138,6 +138,27 @@ def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
     return us, algo, copies
 
 
+def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10):
+    """HBM copy rate of torch's device copy over `nbytes` (read + write), the
+    practical ceiling a streaming kernel can reach on this box, and the
+    calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        dst.copy_(src)
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e))
+    del src, dst
+    return 2 * nbytes / (best * 1e-3) / 1e9
+
+
 def cpu_baseline(spec, tokens: int = 2):
     """The oracle (CPU restatement of the reference path), single thread, on a
     bounded sample: `tokens` decode tokens at positions 0.. of the same model."""
@@ -160,6 +181,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy"], default="all",
+                    help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
@@ -172,18 +195,38 @@ def main() -> int:
         build.build_library()
     engine = ops.ComputeEngine(0)
 
-    log("roofline: Q4_0 GEMV 14336x4096")
-    us, algo, copies = gemv_roofline(engine)
-    achieved = algo / us / 1e3
-    log(f"  {us:.2f} us/launch, {achieved:.0f} GB/s over {copies} weight copies")
+    if args.only == "copy":
+        log(f"copy: {copy_bandwidth():.0f} GB/s (1 GiB device copy, read + write)")
+        return 0
+    if args.only in ("all", "roofline"):
+        log("roofline: Q4_0 GEMV 14336x4096")
+        us, algo, copies = gemv_roofline(engine)
+        achieved = algo / us / 1e3
+        log(f"  {us:.2f} us/launch, {achieved:.0f} GB/s over {copies} weight copies")
+        if args.only == "roofline":
+            return 0
+    if args.only == "all":
+        shapes = {}
+        for n, k in ((4096, 14336), (4096, 4096)):
+            u2, a2, _ = gemv_roofline(engine, n, k)
+            shapes[f"{n}x{k}"] = {"us_per_launch": round(u2, 3), "GB_s": round(a2 / u2 / 1e3, 1)}
+            log(f"  Q4_0 GEMV {n}x{k}: {u2:.2f} us/launch, {a2 / u2 / 1e3:.0f} GB/s")
+        copy_gbs = copy_bandwidth()
+        log(f"  device copy: {copy_gbs:.0f} GB/s")
 
     log("building Llama-3-8B-shape Q4_0 model (random init)")
     t0 = time.time()
     spec = llama3_spec(7, args.layers)
     log(f"  synthesised in {time.time() - t0:.1f} s")
+    if args.only == "bs32":
+        ms32, ctx_sum = decode_bs32(engine, spec, args.steps, args.warmup)
+        log(f"bs=32 ragged: {ms32 / args.steps:.3f} ms/step, {32 * args.steps / (ms32 / 1e3):.1f} tok/s")
+        return 0
     ms, toks = decode_bs1(engine, spec, args.steps, args.warmup)
     tok_s = args.steps / (ms / 1e3)
     log(f"bs=1: {ms / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    if args.only == "bs1":
+        return 0
 
     bs32 = None
     if not args.no_bs32:
@@ -212,7 +255,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
-                     "algorithmic_bytes": algo},
+                     "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
         "cpu_baseline": cpu,
     }
