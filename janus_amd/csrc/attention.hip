@@ -31,7 +31,7 @@ template <> struct KVPad<float> { static constexpr int P = 4; };
 struct AttnArgs {
     const float *q;
     const void *kc, *vc;
-    float *out;
+    void *out;              // [B][H][D] f32, or binary16 when out_f16
     float *ws;              // [B][H][S][D + 2]
     const int32_t *row_base;
     const int32_t *seq_lens;
@@ -40,7 +40,13 @@ struct AttnArgs {
     uint32_t chunk;         // positions per split (multiple of TP)
     uint32_t splits;        // S
     float scale;
+    int out_f16;
 };
+
+__device__ __forceinline__ void put_out(const AttnArgs &a, size_t at, float v) {
+    if (a.out_f16) ((uint16_t *)a.out)[at] = f2h_bits(v);
+    else ((float *)a.out)[at] = v;
+}
 
 __device__ __forceinline__ float to_f(float v) { return v; }
 __device__ __forceinline__ float to_f(_Float16 v) { return (float)v; }
@@ -170,9 +176,9 @@ __global__ __launch_bounds__(THREADS) void attn_partial_kernel(AttnArgs a) {
     const float m = st_m[pg], l = st_l[pg];
     if (a.splits == 1 || len <= a.chunk) {
         float inv = 1.0f / fmaxf(l, 1e-20f);
-        float *o = a.out + ((size_t)b * a.heads + h) * D + pd;
+        const size_t o = ((size_t)b * a.heads + h) * D + pd;
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) o[i] = acc[i] * inv;
+        for (int i = 0; i < DPT; ++i) put_out(a, o + i, acc[i] * inv);
     } else {
         float *w = a.ws + (((size_t)b * a.heads + h) * a.splits + split) * (D + 2);
         if (pd == 0) { w[0] = m; w[1] = l; }
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
         L = fmaf(ws[1], f, L);
         o = fmaf(ws[2 + threadIdx.x], f, o);
     }
-    a.out[((size_t)b * a.heads + h) * D + threadIdx.x] = o / fmaxf(L, 1e-20f);
+    put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
 }
 
 template <typename KV, int D>
@@ -246,10 +252,10 @@ int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t k
     return ensure_attn_ws(ctx, (size_t)batch * heads * splits * (hd + 2) * sizeof(float));
 }
 
-int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, float *out,
+int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
                      uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
-                     float scale) {
+                     float scale, int out_f16) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -263,6 +269,7 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.seq_len = seq_len;
     a.max_seq = max_seq;
     a.scale = scale;
+    a.out_f16 = out_f16;
     uint32_t chunk, splits;
     attention_plan(ctx, batch, kv_heads, max_len, &chunk, &splits);
     a.chunk = chunk;

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 #include <cstring>
 #include <string>
 
@@ -22,6 +23,13 @@ struct janus_ctx {
     // Attention split-K partials; grows on first use and is then reused.
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    // Small-M GEMM split-K partials and per-row-tile arrival counters (the
+    // counters are zero between launches: each launch's last workgroup resets
+    // its own); both grow on first use.
+    void *gemm_ws = nullptr;
+    size_t gemm_ws_bytes = 0;
+    uint32_t *gemm_cnt = nullptr;
+    size_t gemm_cnt_n = 0;
 };
 
 // HBM layout of an uploaded weight. Rows are the output dimension n.
@@ -38,6 +46,11 @@ struct janus_weight {
     size_t bytes = 0;
     const uint8_t *qs = nullptr;
     const uint16_t *sc = nullptr;
+    // MFMA tile copy for the small-M GEMM (smallm.hip), built on first use.
+    void *t32 = nullptr;
+    const uint8_t *t32_qs = nullptr;
+    const uint8_t *t32_side = nullptr;
+    uint32_t t32_chunks = 0;
 };
 
 namespace janus {
@@ -63,6 +76,8 @@ inline size_t act_bytes(int dt) { return dt == JANUS_DT_F16 ? 2 : 4; }
 
 // Grows the context's attention workspace to at least `bytes`.
 int ensure_attn_ws(janus_ctx *ctx, size_t bytes);
+// Grows the small-M GEMM partials to `bytes` and the counters to `tiles`.
+int ensure_gemm_ws(janus_ctx *ctx, size_t bytes, size_t tiles);
 // Returns JANUS_E_NO_DEVICE for a validation-only context (device < 0).
 int need_device(janus_ctx *ctx);
 
@@ -84,6 +99,10 @@ int gemm_dispatch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w
                   int c_dt, uint32_t rows, const float *residual);
 int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w, void *c, int c_dt,
                        uint32_t rows, const float *residual);
+// The MFMA GEMM takes binary16 activations and k % 8 == 0; prepare builds the
+// weight's tile copy (allocates: call outside graph capture).
+bool mfma_gemm_supported(int a_dt, const janus_weight *w);
+int mfma_gemm_prepare(janus_ctx *ctx, const janus_weight *w);
 
 enum { EW_SILU = 0, EW_MUL = 1, EW_ADD = 2, EW_SWIGLU = 3 };
 int rmsnorm_launch(janus_ctx *ctx, const float *in, void *out, int out_dt, const float *gamma, uint32_t batch,
@@ -99,10 +118,11 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t kv_heads, uin
                     uint32_t *splits);
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len);
-int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, float *out,
+// out is f32, or binary16 when out_f16 is set.
+int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
                      uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
-                     float scale);
+                     float scale, int out_f16 = 0);
 int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
                  uint32_t batch, float *out);
 int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie);

@@ -38,6 +38,7 @@ struct janus_model {
     float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h1 = nullptr;
     float *gate = nullptr, *up = nullptr, *logits = nullptr;
     void *xn = nullptr, *act = nullptr;   // act_dtype
+    void *attn16 = nullptr;               // attention output as binary16 (act_dtype F16)
     void *kcache = nullptr, *vcache = nullptr;
     bool kv_external = false;
     size_t layer_kv_elems = 0;
@@ -93,11 +94,14 @@ int forward_rows(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, ui
         if ((e = kv_update_launch(ctx, m->k, m->v, kc, vc, c.kv_dtype, nseq, kvd, 0, c.max_seq_len, nullptr,
                                   m->d_pos)))
             return e;
-        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn, nseq, c.heads, c.kv_heads, c.head_dim, 0,
-                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim))))
+        // attention output in the products' activation dtype
+        const bool a16 = c.act_dtype == JANUS_DT_F16;
+        void *att = a16 ? m->attn16 : (void *)m->attn;
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, att, nseq, c.heads, c.kv_heads, c.head_dim, 0,
+                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), a16)))
             return e;
         // o-proj with the residual add fused: h1 = hidden + attn . Wo^T
-        if ((e = gemm_dispatch(ctx, m->attn, JANUS_DT_F32, L.o, m->h1, JANUS_DT_F32, nseq, m->hidden))) return e;
+        if ((e = gemm_dispatch(ctx, att, c.act_dtype, L.o, m->h1, JANUS_DT_F32, nseq, m->hidden))) return e;
         // feed-forward block (block.rs:370-447)
         if ((e = rmsnorm_launch(ctx, m->h1, m->xn, c.act_dtype, L.ffn_norm, nseq, c.hidden, c.rms_eps))) return e;
         if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.gate, m->gate, JANUS_DT_F32, nseq, nullptr))) return e;
@@ -185,10 +189,10 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
         if ((e = gemv_pair_dispatch(ctx, m->xn, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, c.heads * half,
                                     c.kv_heads * half, half, kvd)))
             return e;
-        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn, 1, c.heads, c.kv_heads, c.head_dim, 0,
-                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim))))
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, 1, c.heads, c.kv_heads, c.head_dim, 0,
+                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), 1)))
             return e;
-        if ((e = gemm_dispatch(ctx, m->attn, JANUS_DT_F32, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
+        if ((e = gemm_dispatch(ctx, m->attn16, JANUS_DT_F16, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
         if ((e = rmsnorm_launch(ctx, m->h1, m->xn, JANUS_DT_F16, L.ffn_norm, 1, c.hidden, c.rms_eps))) return e;
         if ((e = gemv_pair_dispatch(ctx, m->xn, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0,
                                     0)))
@@ -263,7 +267,7 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
               alloc((void **)&m->attn, B * c.hidden * 4) && alloc((void **)&m->h1, B * c.hidden * 4) &&
               alloc((void **)&m->gate, B * c.ffn * 4) && alloc((void **)&m->up, B * c.ffn * 4) &&
               alloc((void **)&m->logits, B * c.vocab * 4) && alloc(&m->xn, B * c.hidden * 4) &&
-              alloc(&m->act, B * c.ffn * 4) &&
+              alloc(&m->act, B * c.ffn * 4) && alloc(&m->attn16, B * c.hidden * 2) &&
               alloc((void **)&m->rope, (size_t)c.max_seq_len * c.head_dim * 4) &&
               alloc((void **)&m->d_pos, B * 4) && alloc((void **)&m->d_lens, B * 4) &&
               alloc((void **)&m->d_tokens, B * 4) && alloc((void **)&m->d_gen, (size_t)c.max_seq_len * 4);
@@ -299,7 +303,7 @@ void janus_model_destroy(janus_model *m) {
     janus_weight_free(m->ctx, m->tok_embd);
     janus_weight_free(m->ctx, m->lm_head);
     for (void *p : {(void *)m->out_norm, (void *)m->hidden, (void *)m->q, (void *)m->k, (void *)m->v,
-                    (void *)m->attn, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
+                    (void *)m->attn, m->attn16, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
                     m->act, m->kv_external ? nullptr : m->kcache, m->kv_external ? nullptr : m->vcache,
                     (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
                     (void *)m->d_tokens, (void *)m->d_gen})
@@ -379,8 +383,17 @@ int janus_model_validate(janus_model *m) {
         if (!L.attn_norm || !L.ffn_norm || !L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down)
             return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
     }
-    if (m->cfg.act_dtype == JANUS_DT_F16) return ensure_fused(m);
-    return JANUS_OK;
+    if (m->cfg.act_dtype != JANUS_DT_F16) return JANUS_OK;
+    if (m->cfg.max_batch > 1) {
+        // tile copies for the batched MFMA products, built before any graph capture
+        for (auto &L : m->layers)
+            for (const janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+                if (mfma_gemm_supported(JANUS_DT_F16, w))
+                    if (int e = mfma_gemm_prepare(m->ctx, w)) return e;
+        if (mfma_gemm_supported(JANUS_DT_F16, m->lm_head))
+            if (int e = mfma_gemm_prepare(m->ctx, m->lm_head)) return e;
+    }
+    return ensure_fused(m);
 }
 
 int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_each) {

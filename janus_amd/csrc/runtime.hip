@@ -37,6 +37,29 @@ int ensure_attn_ws(janus_ctx *ctx, size_t bytes) {
     return JANUS_OK;
 }
 
+int ensure_gemm_ws(janus_ctx *ctx, size_t bytes, size_t tiles) {
+    if (ctx->gemm_ws_bytes < bytes) {
+        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->gemm_ws) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_ws));
+        ctx->gemm_ws = nullptr;
+        ctx->gemm_ws_bytes = 0;
+        size_t sz = bytes < (4u << 20) ? (4u << 20) : bytes;
+        JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->gemm_ws, sz));
+        ctx->gemm_ws_bytes = sz;
+    }
+    if (ctx->gemm_cnt_n < tiles) {
+        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->gemm_cnt) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_cnt));
+        ctx->gemm_cnt = nullptr;
+        ctx->gemm_cnt_n = 0;
+        size_t n = tiles < 4096 ? 4096 : tiles;
+        JANUS_HIP_CHECK(ctx, hipMalloc((void **)&ctx->gemm_cnt, n * sizeof(uint32_t)));
+        JANUS_HIP_CHECK(ctx, hipMemset(ctx->gemm_cnt, 0, n * sizeof(uint32_t)));
+        ctx->gemm_cnt_n = n;
+    }
+    return JANUS_OK;
+}
+
 int need_device(janus_ctx *ctx) {
     if (ctx->device < 0) return fail(ctx, JANUS_E_NO_DEVICE, "validation-only context has no device");
     return JANUS_OK;
@@ -236,6 +259,8 @@ void janus_destroy(janus_ctx *ctx) {
     if (ctx->own_stream) hipStreamSynchronize(ctx->own_stream);
     if (ctx->stream && ctx->stream != ctx->own_stream) hipStreamSynchronize(ctx->stream);
     if (ctx->attn_ws) hipFree(ctx->attn_ws);
+    if (ctx->gemm_ws) hipFree(ctx->gemm_ws);
+    if (ctx->gemm_cnt) hipFree(ctx->gemm_cnt);
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
@@ -388,6 +413,7 @@ int janus_weight_free(janus_ctx *ctx, janus_weight *w) {
         hipStreamSynchronize(ctx->stream);
     }
     if (w->base) hipFree(w->base);
+    if (w->t32) hipFree(w->t32);
     delete w;
     return JANUS_OK;
 }

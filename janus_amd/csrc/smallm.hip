@@ -1,10 +1,615 @@
-// smallm.hip -- products with 2..64 activation rows (ragged decode batches).
+// smallm.hip -- products with 2..64 activation rows (ragged decode batches):
+// the dequant-fused fp16 MFMA GEMM.
+//
+// Replaces the reference's M>1 quantised path, which hands quantised bytes
+// to the f16 GEMM (crates/janus-engine/src/compute/ops/quantized.rs:77-90,
+// 104-117, 131-144; shaders/gemm.wgsl) and so has no correct result to match;
+// parity is "equal to M stacked GEMVs" within fp32 accumulation tolerance.
+//
+// Weight tiles ("T32", built once per weight on first use from the GEMV
+// layout): rows are grouped by 32 and K by chunks; for row group g and chunk c
+// the 64 lanes of a wavefront each load 16 contiguous bytes (1 KiB per
+// wavefront load) that are already the lane's B operand of
+// v_mfma_f32_32x32x16_f16: lane l holds weight row 32g + (l % 32) and the
+// K-half h = l / 32 of each 16-wide MFMA step.
+//   Q4_0 / Q4_K: chunk = 64 K (two 32-element blocks). Per block two words:
+//     elements 8h..8h+7 and 16+8h..16+8h+7, nibbles stored in the order
+//     e0,e2,e4,e6,e1,e3,e5,e7 so that (w >> 4t) & 0x000f000f yields the
+//     natural pair (e_2t, e_2t+1) as binary16 1024 + q.
+//     Q4_0 side data: [g][c][32] u32 = the two blocks' binary16 scales.
+//     Q4_K side data: [g][super-block][32] 16-byte headers (d, dmin, scales).
+//   Q8_0: chunk = 32 K (one block): bytes of elements 8h..8h+7 then
+//     16+8h..16+8h+7; side data [g][c][32] binary16 scales.
+//   F16: chunk = 16 K: the eight binary16 weights 8h..8h+7 of the chunk.
+// Padding rows and K are zero (zero scale), so they add nothing.
+//
+// Kernel: a workgroup is 4 wavefronts on 4 consecutive row groups (128 weight
+// rows) and a range of K "passes". Per pass the activations A[rows][kr]
+// (binary16) are staged in LDS once and shared by the 4 wavefronts; each
+// wavefront streams its weight chunks with 128-bit non-temporal loads,
+// unpacks them in registers into exact binary16 integers, runs
+// 32x32x16 MFMAs with fp32 accumulation per quantisation block, and applies
+// the block scale to the fp32 block result (so products and scales round
+// exactly as the M=1 kernels do). When there are too few row tiles to fill
+// the GPU, K is split over workgroups; the partial tiles go to a workspace
+// with agent-coherent stores and the last workgroup of each row tile (an
+// arrival counter) adds them in fixed split order, so results do not depend
+// on scheduling.
 #include "internal.h"
 
 namespace janus {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+constexpr int WAVES = 4;   // row groups per workgroup
+
+__device__ __forceinline__ jh2 as_h2(uint32_t u) { return __builtin_bit_cast(jh2, u); }
+
+// 8 permuted nibbles -> 8 binary16 (1024 + q) - off, natural element order.
+__device__ __forceinline__ h8 unpack_nib8(uint32_t u, _Float16 off) {
+    const jh2 o = {off, off};
+    jh2 p0 = as_h2((u & 0x000f000fu) | 0x64006400u) - o;
+    jh2 p1 = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - o;
+    jh2 p2 = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - o;
+    jh2 p3 = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - o;
+    return (h8){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// 8 int8 (two words) -> 8 binary16 integers, natural order.
+__device__ __forceinline__ h8 unpack_i8x8(uint32_t lo, uint32_t hi) {
+    const jh2 o = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t c64 = 0x64646464u;
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    jh2 p0 = as_h2(__builtin_amdgcn_perm(lo, c64, 0x00050004u)) - o;
+    jh2 p1 = as_h2(__builtin_amdgcn_perm(lo, c64, 0x00070006u)) - o;
+    jh2 p2 = as_h2(__builtin_amdgcn_perm(hi, c64, 0x00050004u)) - o;
+    jh2 p3 = as_h2(__builtin_amdgcn_perm(hi, c64, 0x00070006u)) - o;
+    return (h8){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+__device__ __forceinline__ f16x mfma(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h8 lds_h8(const _Float16 *p) { return *(const h8 *)p; }
+
+struct GemmArgs {
+    const uint8_t *qs;     // T32 quant chunks [G][C][64][16 B]
+    const uint8_t *side;   // T32 side data (scales / headers)
+    const _Float16 *a;     // activations [rows][k]
+    void *c;               // output [rows][n]
+    const float *resid;    // [rows][n] or null (may alias c)
+    float *ws;             // split-K partials [ksplit][Mpad][Npad]
+    uint32_t *cnt;         // per row tile arrival counters (zero between launches)
+    uint32_t rows, n, k;
+    uint32_t chunks;       // C: chunks per row group
+    uint32_t pass_chunks;  // chunks per LDS pass
+    uint32_t passes_per_wg;
+    uint32_t total_passes;
+    uint32_t ksplit;
+    uint32_t pitch;        // LDS row pitch of A, in halves
+    int c_f16;
+};
+
+// ---- formats ------------------------------------------------------------------
+// W: one chunk of one lane. load() reads it; mma() adds its contribution for
+// MT M-tiles given the LDS A slice (row stride pitch) at chunk offset kl.
+
+struct GQ4_0 {
+    static constexpr int CK = 64;
+    struct W { uint4 q; uint32_t s; };
+    __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
+        const size_t ch = (size_t)g * a.chunks + c;
+        W w;
+        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
+        w.s = ((const uint32_t *)a.side)[ch * 32 + (lane & 31)];
+        return w;
+    }
+    template <int MT>
+    __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                               const float *, uint32_t, f16x (&acc)[MT]) {
+        const int h = lane >> 5, r = lane & 31;
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const h8 b0 = unpack_nib8(q[2 * b], (_Float16)1032.0f);
+            const h8 b1 = unpack_nib8(q[2 * b + 1], (_Float16)1032.0f);
+            const float d = h2f((uint16_t)(b ? (w.s >> 16) : (w.s & 0xffffu)));
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + b * 32 + 8 * h;
+                f16x t = mfma(lds_h8(ap), b0, (f16x){});
+                t = mfma(lds_h8(ap + 16), b1, t);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[mt][v] = fmaf(d, t[v], acc[mt][v]);
+            }
+        }
+    }
+};
+
+struct GQ8_0 {
+    static constexpr int CK = 32;
+    struct W { uint4 q; uint16_t s; };
+    __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
+        const size_t ch = (size_t)g * a.chunks + c;
+        W w;
+        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
+        w.s = ((const uint16_t *)a.side)[ch * 32 + (lane & 31)];
+        return w;
+    }
+    template <int MT>
+    __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                               const float *, uint32_t, f16x (&acc)[MT]) {
+        const int h = lane >> 5, r = lane & 31;
+        const h8 b0 = unpack_i8x8(w.q.x, w.q.y);
+        const h8 b1 = unpack_i8x8(w.q.z, w.q.w);
+        const float d = h2f_q8(w.s);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + 8 * h;
+            f16x t = mfma(lds_h8(ap), b0, (f16x){});
+            t = mfma(lds_h8(ap + 16), b1, t);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[mt][v] = fmaf(d, t[v], acc[mt][v]);
+        }
+    }
+};
+
+// Q4_K: w = (d*sc)*q - dmin*m per 32-element sub-block (shaders/gemm_q4_k.wgsl:82-113);
+// the m term uses the per-(row, sub-block) activation sums staged in LDS.
+struct GQ4_K {
+    static constexpr int CK = 64;
+    struct W { uint4 q; uint4 hdr; };
+    __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
+        const size_t ch = (size_t)g * a.chunks + c;
+        W w;
+        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
+        const size_t sb = (size_t)g * (a.chunks / 4) + c / 4;
+        w.hdr = *(const uint4 *)(a.side + (sb * 32 + (lane & 31)) * 16);
+        return w;
+    }
+    __device__ static void scale_min(const uint4 &hdr, int sub, float &sc, float &mn) {
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        uint32_t scv, mnv;
+        if (sub < 4) {
+            scv = (s0 >> (8 * sub)) & 63u;
+            mnv = (s1 >> (8 * sub)) & 63u;
+        } else {
+            const int i = sub - 4;
+            const uint32_t b8 = (s2 >> (8 * i)) & 0xffu;
+            scv = (b8 & 15u) | ((((s0 >> (8 * i)) & 0xffu) >> 6) << 4);
+            mnv = (b8 >> 4) | ((((s1 >> (8 * i)) & 0xffu) >> 6) << 4);
+        }
+        sc = (float)scv;
+        mn = (float)mnv;
+    }
+    template <int MT>
+    __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                               const float *Ss, uint32_t sub0, f16x (&acc)[MT]) {
+        const int h = lane >> 5, r = lane & 31;
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        const float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
+        const int j = (int)((kl / 64 + sub0 / 2) & 3);   // chunk index within the super-block
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            float sc, mn;
+            scale_min(w.hdr, 2 * j + b, sc, mn);
+            const float ds = d * sc, dm = dmin * mn;
+            const h8 b0 = unpack_nib8(q[2 * b], (_Float16)1024.0f);
+            const h8 b1 = unpack_nib8(q[2 * b + 1], (_Float16)1024.0f);
+            const uint32_t sub = kl / 32 + b;   // sub-block index within the pass
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + b * 32 + 8 * h;
+                f16x t = mfma(lds_h8(ap), b0, (f16x){});
+                t = mfma(lds_h8(ap + 16), b1, t);
+                const float *sx = Ss + (size_t)sub * (MT * 32) + mt * 32 + 4 * h;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const jf4 s4 = *(const jf4 *)(sx + 8 * jj);
+                    acc[mt][4 * jj + 0] = fmaf(-dm, s4.x, fmaf(ds, t[4 * jj + 0], acc[mt][4 * jj + 0]));
+                    acc[mt][4 * jj + 1] = fmaf(-dm, s4.y, fmaf(ds, t[4 * jj + 1], acc[mt][4 * jj + 1]));
+                    acc[mt][4 * jj + 2] = fmaf(-dm, s4.z, fmaf(ds, t[4 * jj + 2], acc[mt][4 * jj + 2]));
+                    acc[mt][4 * jj + 3] = fmaf(-dm, s4.w, fmaf(ds, t[4 * jj + 3], acc[mt][4 * jj + 3]));
+                }
+            }
+        }
+    }
+};
+
+struct GF16 {
+    static constexpr int CK = 16;
+    struct W { uint4 q; };
+    __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
+        const size_t ch = (size_t)g * a.chunks + c;
+        W w;
+        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
+        return w;
+    }
+    template <int MT>
+    __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                               const float *, uint32_t, f16x (&acc)[MT]) {
+        const int h = lane >> 5, r = lane & 31;
+        const h8 b = __builtin_bit_cast(h8, w.q);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma(lds_h8(As + (size_t)(mt * 32 + r) * pitch + kl + 8 * h), b, acc[mt]);
+    }
+};
+
+template <class F> struct Stage { static constexpr int PD = F::CK == 16 ? 16 : 8; };
+
+// Output element (m, n) of wave-tile value v for lane (32x32 MFMA C layout):
+// n = lane % 32, m = 8 * (v / 4) + 4 * (lane / 32) + v % 4.
+__device__ __forceinline__ uint32_t out_row(int mt, int v, int lane) {
+    return (uint32_t)(mt * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3));
+}
+
+template <int MT>
+__device__ __forceinline__ void store_tile(const GemmArgs &a, uint32_t g, int lane, const f16x (&acc)[MT]) {
+    const uint32_t n = g * 32 + (lane & 31);
+    if (n >= a.n) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t m = out_row(mt, v, lane);
+            if (m < a.rows) {
+                float val = acc[mt][v];
+                const size_t at = (size_t)m * a.n + n;
+                if (a.resid) val += a.resid[at];
+                if (a.c_f16) ((uint16_t *)a.c)[at] = f2h_bits(val);
+                else ((float *)a.c)[at] = val;
+            }
+        }
+}
+
+template <class F, int MT>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int PD = Stage<F>::PD;
+    constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t G = (a.n + 31) / 32;
+    const uint32_t tile = blockIdx.x, ks = blockIdx.y;
+    const uint32_t g = tile * WAVES + wave;
+    const bool active = g < G;
+    const uint32_t Mpad = MT * 32;
+    _Float16 *As = (_Float16 *)smem;
+    float *Ss = (float *)(smem + (size_t)Mpad * a.pitch * 2);
+    uint32_t *flag = (uint32_t *)(smem + (size_t)Mpad * a.pitch * 2 +
+                                  (SUMS ? (size_t)(a.pass_chunks * F::CK / 32) * Mpad * 4 : 0));
+
+    f16x acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = (f16x){};
+
+    const uint32_t p_begin = ks * a.passes_per_wg;
+    const uint32_t p_end = min(a.total_passes, p_begin + a.passes_per_wg);
+    for (uint32_t p = p_begin; p < p_end; ++p) {
+        const uint32_t c0 = p * a.pass_chunks, c1 = min(a.chunks, c0 + a.pass_chunks);
+        typename F::W wa[PD], wb[PD];
+        auto load = [&](typename F::W (&w)[PD], uint32_t cs) {
+#pragma unroll
+            for (int i = 0; i < PD; ++i)
+                if (cs + i < c1) w[i] = F::load(a, g, cs + i, lane);
+        };
+        if (active) load(wa, c0);   // in flight while A is staged
+
+        // stage A[0..Mpad)[c0*CK .. c1*CK) as binary16, zero outside rows / k
+        __syncthreads();   // the previous pass is done with LDS
+        const uint32_t kbase = c0 * F::CK, klen = (c1 - c0) * F::CK;
+        const uint32_t segs_per_row = klen / 8, segs = Mpad * segs_per_row;
+        for (uint32_t s = threadIdx.x; s < segs; s += blockDim.x) {
+            const uint32_t m = s / segs_per_row, col = kbase + (s % segs_per_row) * 8;
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (m < a.rows && col < a.k) v = *(const uint4 *)(a.a + (size_t)m * a.k + col);
+            *(uint4 *)(As + (size_t)m * a.pitch + (s % segs_per_row) * 8) = v;
+        }
+        if (SUMS) {
+            __syncthreads();
+            const uint32_t nsub = klen / 32;
+            for (uint32_t i = threadIdx.x; i < nsub * Mpad; i += blockDim.x) {
+                const uint32_t sub = i / Mpad, m = i % Mpad;
+                const _Float16 *p8 = As + (size_t)m * a.pitch + sub * 32;
+                float s = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 32; ++t) s += (float)p8[t];
+                Ss[i] = s;
+            }
+        }
+        __syncthreads();
+        if (!active) continue;
+
+        auto compute = [&](typename F::W (&w)[PD], uint32_t cs) {
+#pragma unroll
+            for (int i = 0; i < PD; ++i)
+                if (cs + i < c1) F::template mma<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, Ss, 0, acc);
+        };
+        uint32_t cs = c0;
+        for (; cs + PD < c1; cs += 2 * PD) {
+            load(wb, cs + PD);
+            compute(wa, cs);
+            if (cs + 2 * PD < c1) load(wa, cs + 2 * PD);
+            compute(wb, cs + PD);
+        }
+        if (cs < c1) compute(wa, cs);
+    }
+
+    if (a.ksplit == 1) {
+        if (active) store_tile<MT>(a, g, lane, acc);
+        return;
+    }
+    // split-K: publish this split's tile, then the last workgroup of the row tile adds them in order
+    const uint32_t Npad = G * 32;
+    if (active) {
+        const uint32_t n = g * 32 + (lane & 31);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                __hip_atomic_store(a.ws + ((size_t)ks * Mpad + out_row(mt, v, lane)) * Npad + n, acc[mt][v],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = (prev == a.ksplit - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (*flag == 0) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (active) {
+        const uint32_t n = g * 32 + (lane & 31);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float s = 0.0f;
+                for (uint32_t j = 0; j < a.ksplit; ++j)
+                    s += __hip_atomic_load(a.ws + ((size_t)j * Mpad + out_row(mt, v, lane)) * Npad + n,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                acc[mt][v] = s;
+            }
+        store_tile<MT>(a, g, lane, acc);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- T32 repack (one thread per lane of a chunk) -----------------------------
+
+// Nibble slot of element j (0..7) within a T32 word.
+__device__ __forceinline__ uint32_t nib_slot(int j) { return (uint32_t)((j >> 1) + 4 * (j & 1)); }
+
+// Q4_0 / Q4_K word: nibbles nib(j), j = 0..7, in T32 slot order.
+template <class GetNib>
+__device__ __forceinline__ uint32_t pack_word(GetNib nib) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w |= (nib(j) & 15u) << (4 * nib_slot(j));
+    return w;
+}
+
+__global__ void t32_q4_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc, uint8_t *dq,
+                                uint32_t *dside, uint32_t n, uint32_t k, uint32_t G, uint32_t C) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)G * C * 64) return;
+    const int lane = (int)(t & 63), h = lane >> 5;
+    const size_t ch = t >> 6;
+    const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
+    const uint32_t r = g * 32 + (lane & 31), nb = k / 32;
+    uint32_t words[4] = {0u, 0u, 0u, 0u};
+    uint16_t s[2] = {0, 0};
+    for (int b = 0; b < 2; ++b) {
+        const uint32_t blk = 2 * c + b;
+        if (r >= n || blk >= nb) continue;
+        const uint8_t *q = qs + ((size_t)r * nb + blk) * 16;
+        words[2 * b] = pack_word([&](int j) { return (uint32_t)(q[8 * h + j] & 15); });
+        words[2 * b + 1] = pack_word([&](int j) { return (uint32_t)(q[8 * h + j] >> 4); });
+        s[b] = sc[(size_t)r * nb + blk];
+    }
+    *(uint4 *)(dq + t * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+    if (lane < 32) dside[ch * 32 + lane] = (uint32_t)s[0] | ((uint32_t)s[1] << 16);
+}
+
+__global__ void t32_q4_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq, uint8_t *dside, uint32_t n,
+                                uint32_t k, uint32_t G, uint32_t C) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)G * C * 64) return;
+    const int lane = (int)(t & 63), h = lane >> 5;
+    const size_t ch = t >> 6;
+    const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
+    const uint32_t r = g * 32 + (lane & 31), nsb = k / 256, sb = c / 4, j = c % 4;
+    uint32_t words[4] = {0u, 0u, 0u, 0u};
+    uint4 hdr = {0u, 0u, 0u, 0u};
+    if (r < n) {
+        const uint8_t *blk = blocks + ((size_t)r * nsb + sb) * 144;
+        const uint8_t *q = blk + 16 + 32 * j;
+        for (int b = 0; b < 2; ++b) {   // sub-block 2j + b: nibble b of bytes 32j + i
+            const int sh = 4 * b;
+            words[2 * b] = pack_word([&](int e) { return (uint32_t)(q[8 * h + e] >> sh); });
+            words[2 * b + 1] = pack_word([&](int e) { return (uint32_t)(q[16 + 8 * h + e] >> sh); });
+        }
+        hdr = *(const uint4 *)blk;
+    }
+    *(uint4 *)(dq + t * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+    if (lane < 32 && j == 0) *(uint4 *)(dside + (((size_t)g * (C / 4) + sb) * 32 + lane) * 16) = hdr;
+}
+
+__global__ void t32_q8_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc, uint8_t *dq,
+                                uint16_t *dside, uint32_t n, uint32_t k, uint32_t G, uint32_t C) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)G * C * 64) return;
+    const int lane = (int)(t & 63), h = lane >> 5;
+    const size_t ch = t >> 6;
+    const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
+    const uint32_t r = g * 32 + (lane & 31), nb = k / 32;
+    uint8_t out[16] = {0};
+    uint16_t s = 0;
+    if (r < n) {
+        const uint8_t *q = qs + ((size_t)r * nb + c) * 32;
+        for (int e = 0; e < 8; ++e) {
+            out[e] = q[8 * h + e];
+            out[8 + e] = q[16 + 8 * h + e];
+        }
+        s = sc[(size_t)r * nb + c];
+    }
+    uint4 v;
+    std::memcpy(&v, out, 16);
+    *(uint4 *)(dq + t * 16) = v;
+    if (lane < 32) dside[ch * 32 + lane] = s;
+}
+
+__global__ void t32_f16_kernel(const uint16_t *__restrict__ src, uint8_t *dq, uint32_t n, uint32_t k, uint32_t G,
+                               uint32_t C) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)G * C * 64) return;
+    const int lane = (int)(t & 63), h = lane >> 5;
+    const size_t ch = t >> 6;
+    const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
+    const uint32_t r = g * 32 + (lane & 31);
+    uint16_t out[8] = {0};
+    if (r < n)
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t kk = c * 16 + 8 * h + e;
+            if (kk < k) out[e] = src[(size_t)r * k + kk];
+        }
+    uint4 v;
+    std::memcpy(&v, out, 16);
+    *(uint4 *)(dq + t * 16) = v;
+}
+
+uint32_t chunk_k(int type) {
+    switch (type) {
+    case JANUS_DT_Q4_0: case JANUS_DT_Q4_K: return 64;
+    case JANUS_DT_Q8_0: return 32;
+    default: return 16;
+    }
+}
+
+// Builds the weight's T32 copy (device memory, kept with the weight).
+int t32_ensure(janus_ctx *ctx, janus_weight *w) {
+    if (w->t32) return JANUS_OK;
+    const uint32_t G = (w->n + 31) / 32, ck = chunk_k(w->type);
+    const uint32_t C = (w->k + ck - 1) / ck;
+    const size_t qbytes = (size_t)G * C * 64 * 16;
+    size_t side = 0;
+    if (w->type == JANUS_DT_Q4_0) side = (size_t)G * C * 32 * 4;
+    else if (w->type == JANUS_DT_Q8_0) side = (size_t)G * C * 32 * 2;
+    else if (w->type == JANUS_DT_Q4_K) side = (size_t)G * (C / 4) * 32 * 16;
+    void *mem = nullptr;
+    JANUS_HIP_CHECK(ctx, hipMalloc(&mem, qbytes + side + 256));
+    uint8_t *dq = (uint8_t *)mem, *ds = (uint8_t *)mem + qbytes;
+    const size_t threads = (size_t)G * C * 64;
+    const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+    switch (w->type) {
+    case JANUS_DT_Q4_0:
+        hipLaunchKernelGGL(t32_q4_0_kernel, grid, block, 0, ctx->stream, w->qs, w->sc, dq, (uint32_t *)ds, w->n,
+                           w->k, G, C);
+        break;
+    case JANUS_DT_Q4_K:
+        hipLaunchKernelGGL(t32_q4_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, ds, w->n, w->k, G, C);
+        break;
+    case JANUS_DT_Q8_0:
+        hipLaunchKernelGGL(t32_q8_0_kernel, grid, block, 0, ctx->stream, w->qs, w->sc, dq, (uint16_t *)ds, w->n,
+                           w->k, G, C);
+        break;
+    default:
+        hipLaunchKernelGGL(t32_f16_kernel, grid, block, 0, ctx->stream, (const uint16_t *)w->qs, dq, w->n, w->k, G,
+                           C);
+        break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(mem);
+        return hip_fail(ctx, e, "t32 repack");
+    }
+    w->t32 = mem;
+    w->t32_qs = dq;
+    w->t32_side = ds;
+    w->t32_chunks = C;
+    return JANUS_OK;
+}
+
+template <class F, int MT>
+int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
+    const uint32_t G = (w->n + 31) / 32;
+    const uint32_t tiles = (G + WAVES - 1) / WAVES;
+    const uint32_t kr = MT == 1 ? 1024 : 512;                  // K per LDS pass
+    a.pass_chunks = kr / F::CK;
+    a.chunks = w->t32_chunks;
+    a.total_passes = (a.chunks + a.pass_chunks - 1) / a.pass_chunks;
+    // split K over workgroups only while there are too few row tiles for ~2 per CU
+    const uint32_t want = 2u * (uint32_t)ctx->num_cus;
+    uint32_t ks = (want + tiles - 1) / tiles;
+    if (ks > a.total_passes) ks = a.total_passes;
+    if (ks < 1) ks = 1;
+    a.passes_per_wg = (a.total_passes + ks - 1) / ks;
+    a.ksplit = (a.total_passes + a.passes_per_wg - 1) / a.passes_per_wg;
+    a.pitch = a.pass_chunks * F::CK + 8;
+    const bool sums = std::is_same<F, GQ4_K>::value;
+    const size_t lds = (size_t)MT * 32 * a.pitch * 2 + (sums ? (size_t)(kr / 32) * MT * 32 * 4 : 0) + 16;
+    if (a.ksplit > 1) {
+        const size_t need = (size_t)a.ksplit * MT * 32 * G * 32 * 4;
+        if (int e = ensure_gemm_ws(ctx, need, tiles)) return e;
+        a.ws = (float *)ctx->gemm_ws;
+        a.cnt = ctx->gemm_cnt;
+    }
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemm_mfma_kernel<F, MT>), dim3(tiles, a.ksplit), dim3(256), lds, ctx->stream, a);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+template <int MT>
+int launch_mt(janus_ctx *ctx, const GemmArgs &a, const janus_weight *w) {
+    switch (w->type) {
+    case JANUS_DT_Q4_0: return launch_mfma<GQ4_0, MT>(ctx, a, w);
+    case JANUS_DT_Q8_0: return launch_mfma<GQ8_0, MT>(ctx, a, w);
+    case JANUS_DT_Q4_K: return launch_mfma<GQ4_K, MT>(ctx, a, w);
+    default: return launch_mfma<GF16, MT>(ctx, a, w);
+    }
+}
+
+}  // namespace
+
+bool mfma_gemm_supported(int a_dt, const janus_weight *w) {
+    if (a_dt != JANUS_DT_F16 || w->k % 8) return false;
+    return w->type == JANUS_DT_Q4_0 || w->type == JANUS_DT_Q8_0 || w->type == JANUS_DT_Q4_K ||
+           w->type == JANUS_DT_F16;
+}
+
+int mfma_gemm_prepare(janus_ctx *ctx, const janus_weight *w) {
+    return t32_ensure(ctx, const_cast<janus_weight *>(w));
+}
 
 int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weight *w, void *c, int c_dt,
                        uint32_t rows, const float *residual) {
+    if (mfma_gemm_supported(a_dt, w)) {
+        if (int e = mfma_gemm_prepare(ctx, w)) return e;
+        GemmArgs g;
+        std::memset(&g, 0, sizeof(g));
+        g.qs = w->t32_qs;
+        g.side = w->t32_side;
+        g.a = (const _Float16 *)a;
+        g.c = c;
+        g.resid = residual;
+        g.rows = rows;
+        g.n = w->n;
+        g.k = w->k;
+        g.c_f16 = c_dt == JANUS_DT_F16;
+        return rows <= 32 ? launch_mt<1>(ctx, g, w) : launch_mt<2>(ctx, g, w);
+    }
+    // f32 activations keep the reference's dtype: one GEMV launch per row
     const size_t as = act_bytes(a_dt) * w->k, cs = act_bytes(c_dt) * w->n;
     for (uint32_t r = 0; r < rows; ++r) {
         int e = gemv_dispatch(ctx, (const uint8_t *)a + r * as, a_dt, w, (uint8_t *)c + r * cs, c_dt,

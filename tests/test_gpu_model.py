@@ -171,3 +171,31 @@ def test_fused_graph_matches_fused_eager(engine):
         outs.append(toks)
         m.close()
     assert outs[0] == outs[1]
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K])
+def test_batched_f16_path_equals_single_sequences(engine, qtype):
+    """Ragged batch with binary16 activations (MFMA GEMM, per-sequence positions)
+    against each sequence run alone on the fused single-sequence GEMV path."""
+    spec = _mini_llama3(17, qtype)
+    rng = np.random.default_rng(19)
+    lens = [5, 12, 8]
+    prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
+    singles = []
+    for pr in prompts:
+        m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for p, t in enumerate(pr):
+            m.forward([t], [p])
+        singles.append(m.logits()[0])
+        m.close()
+    mb = Model(engine, spec, max_seq_len=32, max_batch=3, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    for step in range(max(lens)):
+        mb.forward([pr[min(step, len(pr) - 1)] for pr in prompts], [min(step, len(pr) - 1) for pr in prompts])
+    out = mb.logits(3)
+    for s in range(3):
+        assert _rel_err(out[s], singles[s]) <= 1e-3
+    ref = O.OracleModel(spec, 32, kv_f16=True)
+    for p, t in enumerate(prompts[1]):
+        want = ref.forward(t, p)
+    assert _rel_err(out[1], want) <= REL
+    mb.close()
