@@ -138,6 +138,42 @@ def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
     return us, algo, copies
 
 
+def attention_c4(engine, reps: int = 20):
+    """16 ragged sequences, ctx ~ U[128, 8192], 32 query / 8 KV
+    heads, head_dim 128, fp16 Q/K/V ~ N(0, 1), scale 1/sqrt(128), fp32 softmax,
+    packed into one launch through a prefix-sum row-offset table. Returns
+    (us per launch, algorithmic bytes, total context)."""
+    import torch
+    from janus_amd import ops
+    rng = np.random.default_rng(4)
+    lens = rng.integers(128, 8193, 16)
+    base = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    rows = int(lens.sum())
+    g = torch.Generator(device="cuda").manual_seed(4)
+    k = torch.randn(rows, 8, 128, device="cuda", generator=g).to(torch.float16)
+    v = torch.randn(rows, 8, 128, device="cuda", generator=g).to(torch.float16)
+    q = torch.randn(16, 32, 128, device="cuda", generator=g).to(torch.float16).float()
+    out = torch.empty(16, 32, 128, device="cuda")
+    d_base = torch.from_numpy(base).cuda()
+    d_lens = torch.from_numpy(lens.astype(np.int32)).cuda()
+    call = lambda: ops.compute_attention(engine, q, k, v, out, 16, 0, rows, 32, 8, 128, row_base=d_base,
+                                         seq_lens=d_lens, max_len_hint=int(lens.max()))
+    call()
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(5):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            call()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e) / reps)
+    algo = rows * 8 * 128 * 2 * 2 + q.numel() * 4 + out.numel() * 4
+    del k, v
+    return best * 1e3, algo, rows
+
+
 def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10):
     """HBM copy rate of torch's device copy over `nbytes` (read + write), the
     practical ceiling a streaming kernel can reach on this box, and the
@@ -181,7 +217,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn"], default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -198,6 +234,14 @@ def main() -> int:
     if args.only == "copy":
         log(f"copy: {copy_bandwidth():.0f} GB/s (1 GiB device copy, read + write)")
         return 0
+    attn = None
+    if args.only in ("all", "attn"):
+        a_us, a_bytes, a_rows = attention_c4(engine)
+        attn = {"us_per_launch": round(a_us, 2), "GB_s": round(a_bytes / a_us / 1e3, 1), "ctx_sum": a_rows,
+                "algorithmic_bytes": a_bytes}
+        log(f"attention C4: {a_us:.1f} us/launch, {a_bytes / a_us / 1e3:.0f} GB/s (ctx sum {a_rows})")
+        if args.only == "attn":
+            return 0
     if args.only in ("all", "roofline"):
         log("roofline: Q4_0 GEMV 14336x4096")
         us, algo, copies = gemv_roofline(engine)
@@ -257,6 +301,7 @@ def main() -> int:
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
+        "attention_c4": attn,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -4,15 +4,17 @@
 // compute_qk_scores + softmax + apply_attention in attention.wgsl:62-186 and
 // softmax.wgsl:18-51). Those three passes materialise scores/probabilities in
 // HBM and run the softmax on one thread per head; here:
-//  * grid = (split, kv_head, sequence). A workgroup owns the G = H / KVH query
-//    heads that share one KV head and a contiguous chunk of positions.
-//  * K/V tiles of 64 positions are staged through LDS with 128-bit loads (K
-//    rows padded so per-position dot products read conflict-free), scores are
-//    computed in fp32 from fp16 or fp32 keys, and an online (running max /
-//    running sum) softmax accumulates P.V in fp32 registers.
-//  * Each split writes (m, l, o[D]) partials; a merge kernel combines splits
-//    with the log-sum-exp rule. A sequence covered by one split writes its
-//    output directly.
+//  * One wavefront per (sequence, KV head, split of the context): it owns the
+//    G = H / KVH query heads that share the KV head. Lanes are (position slot,
+//    8-dimension slice), so every K/V load is a 128-bit load and a wavefront
+//    step reads SLOTS whole cache rows; scores are reduced over the slice lanes
+//    with DPP, and each slot runs an online (running max / running sum)
+//    softmax with fp32 P.V accumulators in registers. Batches of steps are
+//    double-buffered; there is no LDS traffic and no barrier.
+//  * Long contexts are split so the launch has ~8 wavefronts per CU; each split
+//    writes (m, l, o[D]) partials and a merge kernel combines them with the
+//    log-sum-exp rule. A sequence covered by one split writes its output
+//    directly.
 //  * Ragged batches: per-sequence row offsets and lengths are device tables,
 //    so all sequences share one launch.
 #include "internal.h"
@@ -21,12 +23,7 @@ namespace janus {
 
 namespace {
 
-constexpr int TP = 64;        // positions per tile
-constexpr int THREADS = 256;
-
-template <typename KV> struct KVPad;
-template <> struct KVPad<_Float16> { static constexpr int P = 8; };
-template <> struct KVPad<float> { static constexpr int P = 4; };
+constexpr int TP = 16;        // split granularity in positions
 
 struct AttnArgs {
     const float *q;
@@ -37,8 +34,9 @@ struct AttnArgs {
     const int32_t *seq_lens;
     uint32_t batch, heads, kv_heads;
     uint32_t seq_len, max_seq;
-    uint32_t chunk;         // positions per split (multiple of TP)
-    uint32_t splits;        // S
+    uint32_t chunk;         // positions per wavefront
+    uint32_t nw;            // wavefronts per workgroup
+    uint32_t splits;        // S: workgroup splits per sequence
     float scale;
     int out_f16;
 };
@@ -48,142 +46,218 @@ __device__ __forceinline__ void put_out(const AttnArgs &a, size_t at, float v) {
     else ((float *)a.out)[at] = v;
 }
 
-__device__ __forceinline__ float to_f(float v) { return v; }
-__device__ __forceinline__ float to_f(_Float16 v) { return (float)v; }
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 
-template <typename KV, int D, int G>
-__global__ __launch_bounds__(THREADS) void attn_partial_kernel(AttnArgs a) {
-    constexpr int KP = D + KVPad<KV>::P;                 // padded K row (elements)
-    constexpr int NPART = G >= 4 ? 1 : 4 / G;            // D-parts per (head, position) in QK
-    constexpr int DP = D / NPART;
-    constexpr int TPH = THREADS / G;                     // PV threads per head
-    constexpr int DPT = TPH >= D ? 1 : D / TPH;          // dims per PV thread
-    constexpr int PS = TPH >= D ? TPH / D : 1;           // position interleave in PV
+// 8 head dimensions of one cached position, as loaded by one lane.
+template <typename KV> struct KVRow;
+template <> struct KVRow<_Float16> {
+    uint4 r;
+    __device__ void load(const _Float16 *p) { r = *(const uint4 *)p; }
+    __device__ float get(int i) const {
+        const uint32_t w = i < 2 ? r.x : i < 4 ? r.y : i < 6 ? r.z : r.w;
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+};
+template <> struct KVRow<float> {
+    jf4 a, b;
+    __device__ void load(const float *p) { a = *(const jf4 *)p; b = *(const jf4 *)(p + 4); }
+    __device__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+};
 
-    __shared__ __align__(16) KV kt[TP * KP];
-    __shared__ __align__(16) KV vt[TP * D];
-    __shared__ __align__(16) float qs[G * D];
-    __shared__ float spart[G * NPART * TP];
-    __shared__ float prob[G * TP];
-    __shared__ float st_m[G], st_l[G], st_alpha[G];
-    __shared__ float comb[PS > 1 ? THREADS * DPT : 1];
+// Sum over the LPP lanes that share a position (every lane receives it).
+template <int LPP> __device__ __forceinline__ float pos_sum(float v) {
+    if (LPP == 16) {
+        v += dpp_f<0x128>(v);   // row_ror:8
+        v += dpp_f<0x124>(v);   // row_ror:4
+        v += dpp_f<0x122>(v);   // row_ror:2
+        v += dpp_f<0x121>(v);   // row_ror:1
+    } else {                    // 8-lane groups
+        v += dpp_f<0x141>(v);   // row_half_mirror: lane i of 8 adds lane 7 - i
+        v += dpp_f<0x4e>(v);    // quad_perm [2,3,0,1]
+        v += dpp_f<0xb1>(v);    // quad_perm [1,0,3,2]
+    }
+    return v;
+}
 
+// Value of lane ^ O for O = 8 (within a 16-lane row), 16 or 32.
+template <int O> __device__ __forceinline__ float lane_xor(float v) {
+    if (O == 8) return dpp_f<0x128>(v);   // row_ror:8 == xor 8 inside a row
+    const uint32_t u = __float_as_uint(v);
+    if (O == 16) {
+        auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((__lane_id() & 16) ? p[0] : p[1]);
+    }
+    auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((__lane_id() & 32) ? p[0] : p[1]);
+}
+
+// Log-sum-exp merge of this lane's (m, l, acc) with lane ^ O's.
+template <int O, int G>
+__device__ __forceinline__ void merge_xor(float (&m)[G], float (&l)[G], float (&acc)[G][8]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float mo = lane_xor<O>(m[g]), lo = lane_xor<O>(l[g]);
+        const float M = fmaxf(m[g], mo);
+        const float fs = M == -INFINITY ? 0.0f : expf(m[g] - M);
+        const float fo = M == -INFINITY ? 0.0f : expf(mo - M);
+        l[g] = l[g] * fs + lo * fo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = acc[g][i] * fs + lane_xor<O>(acc[g][i]) * fo;
+        m[g] = M;
+    }
+}
+
+// A workgroup of NW wavefronts owns (sequence, KV head, workgroup split); its
+// span of NW * chunk positions is divided between the wavefronts. Lane =
+// (position slot, 8-dim slice): a step reads SLOTS whole cache rows with
+// 128-bit loads, scores are reduced over the slice lanes with DPP, and each
+// slot runs an online (running max / running sum) softmax for the G query
+// heads with fp32 P.V accumulators in registers; batches of U steps are
+// double-buffered. Slots, then wavefronts (through LDS, in wavefront order),
+// are merged with the log-sum-exp rule.
+template <typename KV, int D, int G, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
+    extern __shared__ __align__(16) float smem_f[];   // [NW][G][D + 2]
+    constexpr int LPP = D / 8, SLOTS = 64 / LPP;
+    constexpr int KB = sizeof(KV) == 2 ? 1 : 2;            // 16-byte loads per lane per row
+    // steps per batch: sized to the registers a wavefront has at this workgroup size
+    constexpr int U = NW == 16 ? 2 / KB : (G <= 2 ? 8 / KB : (G == 4 ? 4 / KB : 2));
+    constexpr int BATCH = SLOTS * U;                  // positions per batch
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = NW;
+    const int slot = lane / LPP, dl = lane % LPP;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     // lengths beyond the planned splits (or the capacity) are clamped, never read past
-    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * a.chunk);
-    const uint32_t start = split * a.chunk;
-    if (start >= len && !(split == 0 && len == 0)) return;   // len 0: split 0 writes zeros
-    const uint32_t end = min(len, start + a.chunk);
+    const uint32_t span = (uint32_t)nw * a.chunk;
+    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * span);
+    const uint32_t wg_start = split * span;
+    if (wg_start >= len && !(split == 0 && len == 0)) return;   // whole workgroup; len 0: split 0 writes zeros
+    const uint32_t wg_end = min(len, wg_start + span);
+    const uint32_t start = wg_start + wave * a.chunk;
+    const uint32_t end = min(wg_end, start + a.chunk);
     const size_t row0 = (size_t)(a.row_base ? (uint32_t)a.row_base[b] : b * a.max_seq);
-    const uint32_t kvrow = a.kv_heads * D;                // elements per cache row
-    const KV *kc = (const KV *)a.kc + row0 * kvrow + (size_t)kvh * D;
-    const KV *vc = (const KV *)a.vc + row0 * kvrow + (size_t)kvh * D;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t kvrow = a.kv_heads * D;
+    const KV *kc = (const KV *)a.kc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
+    const KV *vc = (const KV *)a.vc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
 
-    // q for the G heads of this KV group
-    for (int i = t; i < G * D; i += THREADS) qs[i] = a.q[((size_t)b * a.heads + kvh * G) * D + i];
-    if (t < G) { st_m[t] = -INFINITY; st_l[t] = 0.0f; }
-
-    // PV ownership: head pg, dims [pd, pd + DPT), positions p % PS == pps
-    const int pg = t / TPH, pr = t % TPH;
-    const int pd = (pr % (D / DPT)) * DPT, pps = pr / (D / DPT);
-    float acc[DPT];
+    float qr[G][8], acc[G][8], m[G], l[G];
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) acc[i] = 0.0f;
-
-    constexpr int VEC = 16 / sizeof(KV);                  // elements per 128-bit load
-    constexpr int CPR = D / VEC;                          // 128-bit chunks per row
-    for (uint32_t p0 = start; p0 < end; p0 += TP) {
-        const int np = (int)min((uint32_t)TP, end - p0);
-        __syncthreads();   // previous tile fully consumed
-        for (int c = t; c < TP * CPR; c += THREADS) {
-            int p = c / CPR, cc = c % CPR;
-            uint4 kv4 = {0u, 0u, 0u, 0u}, vv4 = {0u, 0u, 0u, 0u};
-            if (p < np) {
-                kv4 = *(const uint4 *)(kc + (size_t)(p0 + p) * kvrow + cc * VEC);
-                vv4 = *(const uint4 *)(vc + (size_t)(p0 + p) * kvrow + cc * VEC);
-            }
-            *(uint4 *)(kt + p * KP + cc * VEC) = kv4;
-            *(uint4 *)(vt + p * D + cc * VEC) = vv4;
-        }
-        __syncthreads();
-        // QK partial dots: item -> (head g, part, position p)
-        for (int it = t; it < G * NPART * TP; it += THREADS) {
-            int g = it / (NPART * TP), rest = it % (NPART * TP);
-            int part = rest / TP, p = rest % TP;
-            const KV *kr = kt + p * KP + part * DP;
-            const float *qr = qs + g * D + part * DP;
-            float s0 = 0.0f, s1 = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const float *qp = a.q + ((size_t)b * a.heads + kvh * G + g) * D + 8 * dl;
+        const jf4 q0 = *(const jf4 *)qp, q1 = *(const jf4 *)(qp + 4);
 #pragma unroll
-            for (int d = 0; d < DP; d += 2) {
-                s0 = fmaf(qr[d], to_f(kr[d]), s0);
-                s1 = fmaf(qr[d + 1], to_f(kr[d + 1]), s1);
-            }
-            spart[it] = s0 + s1;
-        }
-        __syncthreads();
-        // softmax statistics: wave w < G owns head w (and w + 4 for G = 8)
-        for (int g = wave; g < G; g += THREADS / 64) {
-            float s = 0.0f;
+        for (int i = 0; i < 4; ++i) { qr[g][i] = q0[i]; qr[g][4 + i] = q1[i]; }
 #pragma unroll
-            for (int part = 0; part < NPART; ++part) s += spart[(g * NPART + part) * TP + lane];
-            s = lane < np ? s * a.scale : -INFINITY;
-            float mt = wave_max(s);
-            float m_old = st_m[g];
-            float m_new = fmaxf(m_old, mt);
-            float e = lane < np ? expf(s - m_new) : 0.0f;
-            prob[g * TP + lane] = e;
-            float lt = wave_sum(e);
-            if (lane == 0) {
-                float alpha = expf(m_old - m_new);
-                st_alpha[g] = alpha;
-                st_l[g] = st_l[g] * alpha + lt;
-                st_m[g] = m_new;
-            }
-        }
-        __syncthreads();
-        // P.V
-        {
-            const float alpha = st_alpha[pg];
-#pragma unroll
-            for (int i = 0; i < DPT; ++i) acc[i] *= alpha;
-            const float *pr_ = prob + pg * TP;
-            for (int p = pps; p < np; p += PS) {
-                float w = pr_[p];
-                const KV *vr = vt + p * D + pd;
-#pragma unroll
-                for (int i = 0; i < DPT; ++i) acc[i] = fmaf(w, to_f(vr[i]), acc[i]);
-            }
-        }
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
     }
-    // combine the PS position-interleaved partial accumulators
-    if (PS > 1) {
-        __syncthreads();
+
+    KVRow<KV> ka[U], va[U], kb[U], vb[U];
+    auto load = [&](KVRow<KV> (&k)[U], KVRow<KV> (&v)[U], uint32_t p0) {
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) comb[t * DPT + i] = acc[i];
-        __syncthreads();
-        if (pps == 0) {
-            for (int s = 1; s < PS; ++s) {
-                int src = pg * TPH + s * (D / DPT) + pr;
+        for (int u = 0; u < U; ++u) {
+            uint32_t p = p0 + u * SLOTS + slot;
+            p = p < end ? p : end - 1;   // masked below; the address stays inside the sequence
+            k[u].load(kc + (size_t)p * kvrow);
+            v[u].load(vc + (size_t)p * kvrow);
+        }
+    };
+    auto consume = [&](const KVRow<KV> (&k)[U], const KVRow<KV> (&v)[U], uint32_t p0) {
+        float s[U][G];
 #pragma unroll
-                for (int i = 0; i < DPT; ++i) acc[i] += comb[src * DPT + i];
+        for (int u = 0; u < U; ++u) {
+            const bool live = p0 + u * SLOTS + slot < end;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    d0 = fmaf(qr[g][i], k[u].get(i), d0);
+                    d1 = fmaf(qr[g][i + 1], k[u].get(i + 1), d1);
+                }
+                const float t = pos_sum<LPP>(d0 + d1);
+                s[u][g] = live ? t * a.scale : -INFINITY;
             }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mx = s[0][g];
+#pragma unroll
+            for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+            const float mn = fmaxf(m[g], mx);
+            if (mn == -INFINITY) continue;   // nothing live in this slot yet
+            const float alpha = expf(m[g] - mn);
+            l[g] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float pu = expf(s[u][g] - mn);
+                l[g] += pu;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pu, v[u].get(i), acc[g][i]);
+            }
+            m[g] = mn;
+        }
+    };
+    if (start < end) {
+        load(ka, va, start);
+        uint32_t p0 = start;
+        for (; p0 + BATCH < end; p0 += 2 * BATCH) {
+            load(kb, vb, p0 + BATCH);
+            consume(ka, va, p0);
+            if (p0 + 2 * BATCH < end) load(ka, va, p0 + 2 * BATCH);
+            consume(kb, vb, p0 + BATCH);
+        }
+        if (p0 < end) consume(ka, va, p0);
+    }
+
+    // merge the slots (lanes lane ^ (LPP * 2^j) hold the same dims of other slots)
+    if (LPP == 8) merge_xor<8, G>(m, l, acc);
+    merge_xor<16, G>(m, l, acc);
+    merge_xor<32, G>(m, l, acc);
+    // merge the wavefronts through LDS, in wavefront order
+    if (slot == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float *r = smem_f + ((size_t)wave * G + g) * (D + 2);
+            if (dl == 0) { r[0] = m[g]; r[1] = l[g]; }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r[2 + 8 * dl + i] = acc[g][i];
         }
     }
     __syncthreads();
-    if (pps != 0) return;
-    const uint32_t h = kvh * G + pg;
-    const float m = st_m[pg], l = st_l[pg];
-    if (a.splits == 1 || len <= a.chunk) {
-        float inv = 1.0f / fmaxf(l, 1e-20f);
-        const size_t o = ((size_t)b * a.heads + h) * D + pd;
+    if (wave != 0 || slot != 0) return;
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) put_out(a, o + i, acc[i] * inv);
-    } else {
-        float *w = a.ws + (((size_t)b * a.heads + h) * a.splits + split) * (D + 2);
-        if (pd == 0) { w[0] = m; w[1] = l; }
+    for (int g = 0; g < G; ++g) {
+        float M = -INFINITY;
+        for (int w = 0; w < nw; ++w) M = fmaxf(M, smem_f[((size_t)w * G + g) * (D + 2)]);
+        float L = 0.0f, o[8];
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) w[2 + pd + i] = acc[i];
+        for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < nw; ++w) {
+                const float *r = smem_f + ((size_t)w * G + g) * (D + 2);
+                const float f = expf(r[0] - M);
+                L = fmaf(r[1], f, L);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = fmaf(r[2 + 8 * dl + i], f, o[i]);
+            }
+        }
+        const uint32_t h = kvh * G + g;
+        if (a.splits == 1 || len <= span) {
+            const float inv = 1.0f / fmaxf(L, 1e-20f);
+            const size_t at = ((size_t)b * a.heads + h) * D + 8 * dl;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) put_out(a, at + i, o[i] * inv);
+        } else {
+            float *w = a.ws + (((size_t)b * a.heads + h) * a.splits + split) * (D + 2);
+            if (dl == 0) { w[0] = M; w[1] = L; }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[2 + 8 * dl + i] = o[i];
+        }
     }
 }
 
@@ -192,9 +266,10 @@ template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     const uint32_t h = blockIdx.x, b = blockIdx.y;
     // lengths beyond the planned splits (or the capacity) are clamped, never read past
-    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * a.chunk);
-    if (len <= a.chunk) return;   // written directly by the partial kernel
-    const uint32_t ns = (len + a.chunk - 1) / a.chunk;
+    const uint32_t span = a.nw * a.chunk;
+    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * span);
+    if (len <= span) return;   // written directly by the partial kernel
+    const uint32_t ns = (len + span - 1) / span;
     const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);
     float M = -INFINITY;
     for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, w[s * (D + 2)]);
@@ -210,12 +285,23 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
 
 template <typename KV, int D>
 int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
-    dim3 grid(a.splits, a.kv_heads, a.batch), block(THREADS);
+    dim3 grid(a.splits, a.kv_heads, a.batch), block(64 * a.nw);
+    const size_t lds = (size_t)a.nw * G * (D + 2) * 4;
+    const bool big = a.nw == 16;
     switch (G) {
-    case 1: hipLaunchKernelGGL((attn_partial_kernel<KV, D, 1>), grid, block, 0, ctx->stream, a); break;
-    case 2: hipLaunchKernelGGL((attn_partial_kernel<KV, D, 2>), grid, block, 0, ctx->stream, a); break;
-    case 4: hipLaunchKernelGGL((attn_partial_kernel<KV, D, 4>), grid, block, 0, ctx->stream, a); break;
-    case 8: hipLaunchKernelGGL((attn_partial_kernel<KV, D, 8>), grid, block, 0, ctx->stream, a); break;
+    case 1:
+        if (big) hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 16>), grid, block, lds, ctx->stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 4>), grid, block, lds, ctx->stream, a);
+        break;
+    case 2:
+        if (big) hipLaunchKernelGGL((attn_decode_kernel<KV, D, 2, 16>), grid, block, lds, ctx->stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<KV, D, 2, 4>), grid, block, lds, ctx->stream, a);
+        break;
+    case 4:
+        if (a.nw == 8) hipLaunchKernelGGL((attn_decode_kernel<KV, D, 4, 8>), grid, block, lds, ctx->stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<KV, D, 4, 4>), grid, block, lds, ctx->stream, a);
+        break;
+    case 8: hipLaunchKernelGGL((attn_decode_kernel<KV, D, 8, 4>), grid, block, lds, ctx->stream, a); break;
     default: return fail(ctx, JANUS_E_INVALID_DIM, "attention: heads / kv_heads must be 1, 2, 4 or 8");
     }
     JANUS_LAUNCH_CHECK(ctx);
@@ -228,26 +314,30 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
 
 }  // namespace
 
-// Chooses the split size so the launch has roughly 2 workgroups per CU.
-void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t kv_heads, uint32_t max_len, uint32_t *chunk_out,
-                    uint32_t *splits_out) {
+// Splits each sequence's context over wavefronts so the launch has roughly 8
+// wavefronts per CU (at least TP positions each). Contexts of up to 1024
+// positions use 16-wavefront (G <= 2) or 8-wavefront (G = 4) workgroups whose
+// wavefronts merge in LDS, so short contexts need no merge launch; otherwise
+// 4-wavefront workgroups, with a merge kernel across workgroup splits.
+void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
+                    uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out) {
     if (max_len == 0) max_len = 1;
-    uint64_t groups = (uint64_t)batch * kv_heads;
-    uint64_t want = (uint64_t)ctx->num_cus * 2;
-    uint32_t splits = (uint32_t)((want + groups - 1) / groups);
-    uint32_t max_splits = (max_len + TP - 1) / TP;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    uint32_t chunk = (max_len + splits - 1) / splits;
+    const uint64_t groups = (uint64_t)batch * kv_heads;
+    const uint64_t want = (uint64_t)ctx->num_cus * 8;
+    uint64_t chunk = (max_len * groups + want - 1) / want;
     chunk = (chunk + TP - 1) / TP * TP;
-    *chunk_out = chunk;
-    *splits_out = (max_len + chunk - 1) / chunk;
+    const uint32_t G = heads / kv_heads;
+    const uint32_t nw = max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4));
+    if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
+    *chunk_out = (uint32_t)chunk;
+    *nw_out = nw;
+    *splits_out = (uint32_t)((max_len + chunk * nw - 1) / (chunk * nw));
 }
 
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len) {
-    uint32_t chunk, splits;
-    attention_plan(ctx, batch, kv_heads, max_len, &chunk, &splits);
+    uint32_t chunk, nw, splits;
+    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits);
     if (splits <= 1) return JANUS_OK;
     return ensure_attn_ws(ctx, (size_t)batch * heads * splits * (hd + 2) * sizeof(float));
 }
@@ -270,9 +360,10 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.max_seq = max_seq;
     a.scale = scale;
     a.out_f16 = out_f16;
-    uint32_t chunk, splits;
-    attention_plan(ctx, batch, kv_heads, max_len, &chunk, &splits);
+    uint32_t chunk, nw, splits;
+    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits);
     a.chunk = chunk;
+    a.nw = nw;
     a.splits = splits;
     a.ws = nullptr;
     if (splits > 1) {

@@ -80,16 +80,21 @@ __device__ __forceinline__ float load16h_perm(const _Float16 *p, jh2 *dst) {
 // ---------------------------------------------------------------------------
 // Writes x[0..k) into LDS: element e goes to block e/32, slot e%32. For f16
 // with PERM, each group of four (a,b,c,d) is stored as (a,c,b,d) so a u32 of
-// packed nibbles maps onto (x[i], x[i+2]) pairs. sx16[g] = sum of x[16g..16g+16).
-template <typename XIN, typename XT, bool PERM>
-__device__ void stage_x(const XIN *__restrict__ x, uint32_t k, XT *xs, float *sx16) {
+// packed nibbles maps onto (x[i], x[i+2]) pairs. sx16[g] = sum of the stored
+// values x[16g..16g+16). With NORM the stored value is (x / rms) * gamma,
+// the RMSNorm of shaders/activations.wgsl:114,128.
+template <typename XIN, typename XT, bool PERM, bool NORM = false>
+__device__ void stage_x(const XIN *__restrict__ x, uint32_t k, XT *xs, float *sx16,
+                        const float *__restrict__ gamma = nullptr, float rms = 1.0f) {
     const int groups = (int)((k + 15) / 16);
     for (int g = threadIdx.x; g < groups; g += blockDim.x) {
         float v[16];
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             uint32_t e = (uint32_t)g * 16 + t;
-            v[t] = e < k ? (float)x[e] : 0.0f;
+            float f = e < k ? (float)x[e] : 0.0f;
+            if (NORM) f = e < k ? (f / rms) * gamma[e] : 0.0f;
+            v[t] = (float)(XT)f;   // the value the products will read
         }
         float s = 0.0f;
 #pragma unroll
@@ -492,13 +497,23 @@ __device__ __forceinline__ float reduce_rows(float (&v)[R], int li, int &ridx) {
     return s;
 }
 
-enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3 };
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3, EPI_ARGMAX = 4 };
+
+// Order-preserving key of a float (larger value -> larger key); NaN maps to 0
+// so it never wins. Packed with the row index below it, the maximum key is
+// the largest value and, among equal values, the last index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t k = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    return ((uint64_t)k << 32) | idx;
+}
 
 struct GemvArgs {
     WPtr w;
     const void *x;       // activation [k]
     void *y;             // output [n] (EPI_SWIGLU: [n / 2])
     const float *resid;  // residual [n] (EPI_RESIDUAL)
+    unsigned long long *best;   // EPI_ARGMAX: running max of argmax_key, reset by the consumer
     uint32_t n, k;
     uint32_t units;      // units per row
     int out_f16;
@@ -511,6 +526,9 @@ struct GemvArgs {
     const int32_t *d_pos;
     uint32_t q_pairs, k_pairs, half_hd, kv_row;
     int kv_f16;
+    // fused RMSNorm of x (f32) with gamma, eps (the LDS kernel)
+    const float *gamma;
+    float eps;
 };
 
 template <class F, typename XIN, typename XT, int LPR, int R, int BPL_MAX>
@@ -617,8 +635,14 @@ __device__ __forceinline__ float reduce_wave_rows(float (&v)[R], int lane, int &
 // steady-state loop is branch-free: the next group's weights are loaded while
 // the current group is reduced, so the loads of one stage stay in flight
 // behind the arithmetic of the other.
-template <class F, typename XT, int BPL, int R, bool FULL>
-__device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
+// XMODE 0: each lane keeps its units of x in registers, read once from global
+// memory. XMODE 1: the same, read once from the LDS staging (xs, sx16) that
+// stage() fills. XMODE 2: x is read from LDS per unit at every use (long rows,
+// where x in registers would cost occupancy). stage() is called by every
+// wavefront of the workgroup after the first weight loads are issued.
+template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int>
+__device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = nullptr,
+                                              const float *sx16 = nullptr, StageFn stage = 0) {
     const int lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
@@ -645,12 +669,20 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
             for (int i = 0; i < BPL; ++i) w[i][r] = F::load(a.w, (size_t)row * units + uu[i]);
         }
     };
-    const uint32_t mine = (groups - 1 - wave) / nwaves + 1;   // groups this wavefront owns
-    load(wa, wave);
+    const bool has = wave < groups;
+    const uint32_t mine = has ? (groups - 1 - wave) / nwaves + 1 : 0;   // groups this wavefront owns
+    if (has) load(wa, wave);
+    if constexpr (XMODE != 0) stage();
+    if (!has) return;
 
-    XR xr[BPL];
+    XR xr[XMODE == 2 ? 1 : BPL];
+    if constexpr (XMODE == 0) {
 #pragma unroll
-    for (int i = 0; i < BPL; ++i) xr[i] = F::loadx_g((const XT *)a.x, uu[i]);
+        for (int i = 0; i < BPL; ++i) xr[i] = F::loadx_g((const XT *)a.x, uu[i]);
+    } else if constexpr (XMODE == 1) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) xr[i] = F::loadx(xs, sx16, uu[i]);
+    }
 
     // Row written by this lane after the reduction (a static function of the lane).
     const int my_ridx = R == 1 ? 0 : R == 2 ? (lane >> 5) : (((lane >> 5) << 1) | ((lane >> 4) & 1));
@@ -670,17 +702,22 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
         }
         return make_float2(0.0f, 0.0f);
     };
+    uint64_t best = 0;   // EPI_ARGMAX: this lane's running maximum key
     auto consume = [&](WT (&w)[BPL][R], uint32_t g, float2 side) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < BPL; ++i)
+        for (int i = 0; i < BPL; ++i) {
+            XR xv;
+            if constexpr (XMODE == 2) xv = F::loadx(xs, sx16, uu[i]);
+            else xv = xr[i];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float d = F::dot(w[i][r], xr[i]);
+                const float d = F::dot(w[i][r], xv);
                 acc[r] = ok[i] ? acc[r] + d : acc[r];
             }
+        }
         int ridx;
         float s = reduce_wave_rows<R>(acc, lane, ridx);
         if (R == 2 && a.epi >= EPI_QKV_ROPE) {
@@ -731,6 +768,10 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
             s += side.x;
             if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
             else ((float *)a.y)[row] = s;
+            if (a.epi == EPI_ARGMAX) {
+                const uint64_t key = argmax_key(s, row);
+                best = key > best ? key : best;
+            }
         }
     };
 
@@ -749,8 +790,17 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a) {
         load(wb, g + nwaves);
         consume(wa, g, ra);
         consume(wb, g + nwaves, rb);
-    } else {
+    } else if (it < mine) {
         consume(wa, g, ra);
+    }
+    if (a.epi == EPI_ARGMAX) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t other = ((uint64_t)(uint32_t)shfl_xor((int)(best >> 32), o) << 32) |
+                                   (uint32_t)shfl_xor((int)(best & 0xffffffffu), o);
+            best = other > best ? other : best;
+        }
+        if (lane == 0 && best) atomicMax(a.best, (unsigned long long)best);
     }
 }
 
@@ -760,6 +810,97 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
     if (wave >= (a.n + R - 1) / R) return;
     if (a.units == 64u * BPL) gemv_reg_body<F, XT, BPL, R, true>(a);
     else gemv_reg_body<F, XT, BPL, R, false>(a);
+}
+
+// Vectorised staging of binary16 x for the LDS kernel: each thread handles
+// groups of 16 elements (16-byte global loads of x, and of gamma when
+// normalising) and writes them with 8-byte LDS stores in the layout of
+// stage_x; sx16 gets the 16-element sums of the stored values.
+template <bool PERM, bool NORM>
+__device__ void stage_x16(const void *__restrict__ xin, uint32_t k, _Float16 *xs, float *sx16,
+                          const float *__restrict__ gamma, float rms) {
+    const uint32_t g16 = (k + 15) / 16;
+    for (uint32_t g = threadIdx.x; g < g16; g += blockDim.x) {
+        float v[16];
+        const uint32_t e0 = g * 16;
+        if (NORM) {
+            const float *x = (const float *)xin;
+            if (e0 + 16 <= k) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const jf4 xa = *(const jf4 *)(x + e0 + 4 * q), ga = *(const jf4 *)(gamma + e0 + 4 * q);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) v[4 * q + t] = (xa[t] / rms) * ga[t];
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) v[t] = e0 + t < k ? (x[e0 + t] / rms) * gamma[e0 + t] : 0.0f;
+            }
+        } else {
+            const _Float16 *x = (const _Float16 *)xin;
+            if (e0 + 16 <= k) {
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const uint4 u = *(const uint4 *)(x + e0 + 8 * q);
+                    const jh2 h[4] = {as_h2(u.x), as_h2(u.y), as_h2(u.z), as_h2(u.w)};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) { v[8 * q + 2 * t] = (float)h[t].x; v[8 * q + 2 * t + 1] = (float)h[t].y; }
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) v[t] = e0 + t < k ? (float)x[e0 + t] : 0.0f;
+            }
+        }
+        _Float16 hv[16];
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            hv[t] = (_Float16)v[t];
+            s += (float)hv[t];
+        }
+        sx16[g] = s;
+        _Float16 *dst = xs + (e0 / 32) * XLayout<_Float16>::STRIDE + (e0 % 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const jh4 o = PERM ? (jh4){hv[4 * q], hv[4 * q + 2], hv[4 * q + 1], hv[4 * q + 3]}
+                               : (jh4){hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+            *(jh4 *)(dst + 4 * q) = o;
+        }
+    }
+}
+
+// LDS-staged variant for binary16 products: 512-thread workgroups, x staged
+// once per workgroup (optionally RMS-normalised on the way: the sum of squares
+// is reduced over the workgroup in a fixed order, then x / rms * gamma is
+// rounded to binary16). Up to 4 units per lane, each lane then keeps its units
+// in registers; longer rows read their units from LDS at every use.
+template <class F, int BPL, int R, bool NORM>
+__global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    _Float16 *xs = (_Float16 *)smem;
+    float *sx16 = (float *)(smem + ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~15u));
+    float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
+    auto stage = [&]() {
+        if constexpr (NORM) {
+            const float *x = (const float *)a.x;
+            float ss = 0.0f;
+            for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+            ss = wave_sum(ss);
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+            for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += red[w];
+            const float rms = sqrtf(tot / (float)a.k + a.eps);
+            stage_x16<F::PERM, true>(x, a.k, xs, sx16, a.gamma, rms);
+        } else {
+            stage_x16<F::PERM, false>(a.x, a.k, xs, sx16, nullptr, 1.0f);
+        }
+        __syncthreads();
+    };
+    constexpr int XMODE = BPL <= 4 ? 1 : 2;
+    if (a.units == 64u * BPL) gemv_reg_body<F, _Float16, BPL, R, true, XMODE>(a, xs, sx16, stage);
+    else gemv_reg_body<F, _Float16, BPL, R, false, XMODE>(a, xs, sx16, stage);
 }
 
 // Generic fallback for F16 weights whose k is not a multiple of 8: one
@@ -868,10 +1009,72 @@ int launch_reg_fmt(janus_ctx *ctx, const GemvArgs &a, bool &done) {
     return JANUS_OK;
 }
 
+// LDS-staged kernel: grid = the workgroups that fit at once (occupancy of the
+// compiled kernel), each wavefront walking several row groups.
+template <class F, int BPL, int R>
+int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
+    static int per_cu[2] = {0, 0};
+    const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
+    if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
+    int &pc = per_cu[norm ? 1 : 0];
+    if (pc == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 512, 40 * 1024) != hipSuccess || nb < 1) nb = 1;
+        pc = nb > 2 ? 2 : nb;
+    }
+    const uint32_t groups = (a.n + R - 1) / R;
+    uint32_t blocks = (groups + 7) / 8;
+    const uint32_t cap = (uint32_t)ctx->num_cus * pc;
+    if (blocks > cap) blocks = cap;
+    if (norm) hipLaunchKernelGGL((gemv_lds_kernel<F, BPL, R, true>), dim3(blocks), dim3(512), lds, ctx->stream, a);
+    else hipLaunchKernelGGL((gemv_lds_kernel<F, BPL, R, false>), dim3(blocks), dim3(512), lds, ctx->stream, a);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+// Units per lane = ceil(units / 64), up to 8; two rows per wavefront step up
+// to 4 units per lane (always two for the paired-row epilogues).
+template <class F>
+int launch_lds_fmt(janus_ctx *ctx, const GemvArgs &a, bool norm, bool pair, bool &done) {
+    const int bpl = (int)((a.units + 63) / 64);
+    done = bpl <= 8;
+    if (!done) return JANUS_OK;
+    if (pair) {
+        switch (bpl) {
+        case 1: return launch_lds<F, 1, 2>(ctx, a, norm);
+        case 2: return launch_lds<F, 2, 2>(ctx, a, norm);
+        case 3: return launch_lds<F, 3, 2>(ctx, a, norm);
+        case 4: return launch_lds<F, 4, 2>(ctx, a, norm);
+        case 5: return launch_lds<F, 5, 2>(ctx, a, norm);
+        case 6: return launch_lds<F, 6, 2>(ctx, a, norm);
+        case 7: return launch_lds<F, 7, 2>(ctx, a, norm);
+        default: return launch_lds<F, 8, 2>(ctx, a, norm);
+        }
+    }
+    switch (bpl) {
+    case 1: return launch_lds<F, 1, 4>(ctx, a, norm);
+    case 2: return launch_lds<F, 2, 2>(ctx, a, norm);
+    case 3: return launch_lds<F, 3, 2>(ctx, a, norm);
+    case 4: return launch_lds<F, 4, 2>(ctx, a, norm);
+    case 5: return launch_lds<F, 5, 1>(ctx, a, norm);
+    case 6: return launch_lds<F, 6, 1>(ctx, a, norm);
+    case 7: return launch_lds<F, 7, 1>(ctx, a, norm);
+    default: return launch_lds<F, 8, 1>(ctx, a, norm);
+    }
+}
+
 template <class F>
 int launch_gemv(janus_ctx *ctx, GemvArgs a, int x_dt) {
     bool done = false;
     int e;
+    // binary16 rows longer than 4 units per lane: LDS staging keeps x out of
+    // the registers (more wavefronts per SIMD)
+    if (x_dt == JANUS_DT_F16 && ctx->gemv_lds && a.units > 4 * 64) {
+        e = launch_lds_fmt<F>(ctx, a, false, false, done);
+        if (done || e) return e;
+    }
     if (x_dt == JANUS_DT_F16) e = launch_reg_fmt<F, _Float16>(ctx, a, done);
     else e = launch_reg_fmt<F, float>(ctx, a, done);
     if (done || e) return e;
@@ -902,9 +1105,11 @@ namespace janus {
 
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
                        void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
-                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row) {
+                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma, float eps) {
     GemvArgs a;
     std::memset(&a, 0, sizeof(a));
+    a.gamma = gamma;
+    a.eps = eps;
     a.w.qs = w->qs;
     a.w.sc = w->sc;
     a.x = x;
@@ -923,16 +1128,53 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
     a.half_hd = half_hd;
     a.kv_row = kv_row;
     if (w->n % 2) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: odd row count");
+    const bool norm = gamma != nullptr;
+    bool done = false;
+    int e = JANUS_OK;
     switch (w->type) {
-    case JANUS_DT_Q4_0: a.units = w->k / 32; return launch_pair_fmt<FQ4_0, _Float16>(ctx, a);
-    case JANUS_DT_Q8_0: a.units = w->k / 32; return launch_pair_fmt<FQ8_0, _Float16>(ctx, a);
-    case JANUS_DT_Q4_K: a.units = w->k / 32; return launch_pair_fmt<FQ4_K, _Float16>(ctx, a);
+    case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, norm, true, done); break;
+    case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, norm, true, done); break;
+    case JANUS_DT_Q4_K: a.units = w->k / 32; e = launch_lds_fmt<FQ4_K>(ctx, a, norm, true, done); break;
     case JANUS_DT_F16:
         if (w->k % 8) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: F16 rows need k % 8 == 0");
         a.units = w->k / 8;
-        return launch_pair_fmt<FF16, _Float16>(ctx, a);
+        e = launch_lds_fmt<FF16>(ctx, a, norm, true, done);
+        break;
     default: return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "paired gemv: unsupported weight type");
     }
+    if (!e && !done) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: row too long");
+    return e;
+}
+
+int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
+                       unsigned long long *best) {
+    GemvArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.w.qs = w->qs;
+    a.w.sc = w->sc;
+    a.x = x;
+    a.y = y;
+    a.n = w->n;
+    a.k = w->k;
+    a.epi = best ? EPI_ARGMAX : EPI_STORE;
+    a.best = best;
+    a.gamma = gamma;
+    a.eps = eps;
+    bool done = false;
+    int e = JANUS_OK;
+    switch (w->type) {
+    case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, true, false, done); break;
+    case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, true, false, done); break;
+    case JANUS_DT_Q4_K: a.units = w->k / 32; e = launch_lds_fmt<FQ4_K>(ctx, a, true, false, done); break;
+    case JANUS_DT_F16:
+        if (w->k % 8) return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: F16 rows need k % 8 == 0");
+        a.units = w->k / 8;
+        e = launch_lds_fmt<FF16>(ctx, a, true, false, done);
+        break;
+    default: return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "normed gemv: unsupported weight type");
+    }
+    if (!e && !done) return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: row too long");
+    return e;
 }
 
 int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,

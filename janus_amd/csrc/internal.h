@@ -20,16 +20,15 @@ struct janus_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string last_error;
+    // binary16 M = 1 products with long rows use the LDS-staged kernel
+    // (JANUS_GEMV_KERNEL=reg selects the register-resident one instead).
+    bool gemv_lds = true;
     // Attention split-K partials; grows on first use and is then reused.
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
-    // Small-M GEMM split-K partials and per-row-tile arrival counters (the
-    // counters are zero between launches: each launch's last workgroup resets
-    // its own); both grow on first use.
+    // Small-M GEMM split-K partials; grows on first use.
     void *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
-    uint32_t *gemm_cnt = nullptr;
-    size_t gemm_cnt_n = 0;
 };
 
 // HBM layout of an uploaded weight. Rows are the output dimension n.
@@ -76,19 +75,27 @@ inline size_t act_bytes(int dt) { return dt == JANUS_DT_F16 ? 2 : 4; }
 
 // Grows the context's attention workspace to at least `bytes`.
 int ensure_attn_ws(janus_ctx *ctx, size_t bytes);
-// Grows the small-M GEMM partials to `bytes` and the counters to `tiles`.
-int ensure_gemm_ws(janus_ctx *ctx, size_t bytes, size_t tiles);
+// Grows the small-M GEMM split-K partials to at least `bytes`.
+int ensure_gemm_ws(janus_ctx *ctx, size_t bytes);
 // Returns JANUS_E_NO_DEVICE for a validation-only context (device < 0).
 int need_device(janus_ctx *ctx);
 
 // M = 1 product (gemv.hip). residual may be null; when set, y must be F32.
 int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
                   const float *residual);
-// Paired-row M = 1 products with x in f16: epi 0 = fused QKV with RoPE and KV
-// append (q rotated into y, f32), epi 1 = fused gate/up with SwiGLU into y.
+// Paired-row M = 1 products: epi 0 = fused QKV with RoPE and KV append (q
+// rotated into y, f32), epi 1 = fused gate/up with SwiGLU into y. x is f16,
+// or, with gamma set, the f32 residual stream RMS-normalised in the kernel.
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
                        void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
-                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row);
+                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma = nullptr,
+                       float eps = 0.0f);
+// M = 1 product of RMSNorm(x, gamma, eps) (x f32) into y (f32). With best
+// set, the outputs are also folded into *best as the running maximum of
+// (order-preserving key << 32 | row): the greedy last-max argmax
+// (model/sampler.rs:784-795); *best must be 0 before the launch.
+int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
+                       unsigned long long *best);
 // Row layout of an uploaded weight (bytes of quants, binary16 scales per row).
 size_t weight_qs_row_bytes(int type, uint32_t k);
 size_t weight_sc_row_elems(int type, uint32_t k);
@@ -114,8 +121,8 @@ int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, voi
                      uint32_t batch, uint32_t row_elems, uint32_t position, uint32_t max_seq,
                      const int32_t *row_base, const int32_t *positions);
 // Attention split sizing shared by the launch and workspace reservation.
-void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t kv_heads, uint32_t max_len, uint32_t *chunk,
-                    uint32_t *splits);
+void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
+                    uint32_t *chunk, uint32_t *nw, uint32_t *splits);
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len);
 // out is f32, or binary16 when out_f16 is set.

@@ -44,6 +44,7 @@ struct janus_model {
     size_t layer_kv_elems = 0;
     float *rope = nullptr;
     int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_gen = nullptr;
+    unsigned long long *d_best = nullptr;   // graph decode: folded argmax of the LM head (zero between steps)
     std::vector<uint32_t> h_pos;   // graph mode: host mirror of device positions
     uint32_t graph_nseq = 0;
     hipGraph_t graph = nullptr;
@@ -64,11 +65,18 @@ int parse_layer_name(const std::string &name, uint32_t *layer, std::string *rest
     return 1;
 }
 
-__global__ void advance_pos_kernel(int32_t *pos, int32_t *lens, uint32_t n) {
+// End of a graph decode step: advance positions; when the LM head folded the
+// argmax into *best, take the token from it and clear it for the next step.
+__global__ void advance_pos_kernel(int32_t *pos, int32_t *lens, uint32_t n, unsigned long long *best,
+                                   int32_t *tokens) {
     uint32_t i = threadIdx.x;
     if (i < n) {
         pos[i] += 1;
         lens[i] = pos[i] + 1;
+        if (best) {
+            tokens[i] = (int32_t)(uint32_t)(best[i] & 0xffffffffull);
+            best[i] = 0;
+        }
     }
 }
 
@@ -171,10 +179,21 @@ int ensure_fused(janus_model *m) {
     return JANUS_OK;
 }
 
+// The LM head runs as one LDS-staged GEMV with the final RMSNorm fused in
+// (and optionally the argmax) when its rows fit that kernel.
+bool can_fold_head(const janus_model *m) {
+    const janus_weight *w = m->lm_head;
+    if (w->type != JANUS_DT_F16 || w->k % 8) return false;
+    return (w->k / 8 + 63) / 64 <= 8;
+}
+
 // Single-sequence step over the fused weights (f16 activations): per layer
-// rmsnorm, QKV+RoPE+KV append, attention, o-proj+residual, rmsnorm,
-// gate/up+SwiGLU, down-proj+residual.
-int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t max_len) {
+// QKV (with the attention RMSNorm in its prologue and RoPE + KV append in its
+// epilogue), attention, o-proj + residual, gate/up (FFN RMSNorm prologue,
+// SwiGLU epilogue), down-proj + residual; the final RMSNorm runs in the LM
+// head's prologue.
+int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t max_len,
+                   bool fold_argmax = false) {
     janus_ctx *ctx = m->ctx;
     const janus_model_config &c = m->cfg;
     const uint32_t kvd = c.kv_heads * c.head_dim, half = c.head_dim / 2;
@@ -185,23 +204,26 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
         const janus_model::Layer &L = m->layers[l];
         void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
         void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
-        if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, L.attn_norm, 1, c.hidden, c.rms_eps))) return e;
-        if ((e = gemv_pair_dispatch(ctx, m->xn, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, c.heads * half,
-                                    c.kv_heads * half, half, kvd)))
+        if ((e = gemv_pair_dispatch(ctx, m->hidden, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, c.heads * half,
+                                    c.kv_heads * half, half, kvd, L.attn_norm, c.rms_eps)))
             return e;
         if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, 1, c.heads, c.kv_heads, c.head_dim, 0,
                                   c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), 1)))
             return e;
         if ((e = gemm_dispatch(ctx, m->attn16, JANUS_DT_F16, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
-        if ((e = rmsnorm_launch(ctx, m->h1, m->xn, JANUS_DT_F16, L.ffn_norm, 1, c.hidden, c.rms_eps))) return e;
-        if ((e = gemv_pair_dispatch(ctx, m->xn, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0,
-                                    0)))
+        if ((e = gemv_pair_dispatch(ctx, m->h1, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0,
+                                    0, L.ffn_norm, c.rms_eps)))
             return e;
         if ((e = gemm_dispatch(ctx, m->act, JANUS_DT_F16, L.down, m->hidden, JANUS_DT_F32, 1, m->h1))) return e;
     }
+    if (can_fold_head(m))
+        return gemv_norm_dispatch(ctx, m->hidden, m->out_norm, c.rms_eps, m->lm_head, m->logits,
+                                  fold_argmax ? m->d_best : nullptr);
     if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, m->out_norm, 1, c.hidden, c.rms_eps))) return e;
     return gemm_dispatch(ctx, m->xn, JANUS_DT_F16, m->lm_head, m->logits, JANUS_DT_F32, 1, nullptr);
 }
+
+bool can_fold_argmax(const janus_model *m) { return can_fold_head(m); }
 
 bool use_fused1(const janus_model *m, uint32_t nseq) {
     if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready) return false;
@@ -270,7 +292,8 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
               alloc(&m->act, B * c.ffn * 4) && alloc(&m->attn16, B * c.hidden * 2) &&
               alloc((void **)&m->rope, (size_t)c.max_seq_len * c.head_dim * 4) &&
               alloc((void **)&m->d_pos, B * 4) && alloc((void **)&m->d_lens, B * 4) &&
-              alloc((void **)&m->d_tokens, B * 4) && alloc((void **)&m->d_gen, (size_t)c.max_seq_len * 4);
+              alloc((void **)&m->d_tokens, B * 4) && alloc((void **)&m->d_gen, (size_t)c.max_seq_len * 4) &&
+              alloc((void **)&m->d_best, B * 8) && hipMemset(m->d_best, 0, B * 8) == hipSuccess;
     m->layer_kv_elems = B * c.max_seq_len * kvd;
     size_t kv_bytes = (size_t)c.layers * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
     ok = ok && alloc(&m->kcache, kv_bytes) && alloc(&m->vcache, kv_bytes);
@@ -306,7 +329,7 @@ void janus_model_destroy(janus_model *m) {
                     (void *)m->attn, m->attn16, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
                     m->act, m->kv_external ? nullptr : m->kcache, m->kv_external ? nullptr : m->vcache,
                     (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
-                    (void *)m->d_tokens, (void *)m->d_gen})
+                    (void *)m->d_tokens, (void *)m->d_gen, (void *)m->d_best})
         if (p) hipFree(p);
     delete m;
 }
@@ -516,11 +539,13 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
         ctx->stream = user;
         return hip_fail(ctx, be, "hipStreamBeginCapture");
     }
-    e = use_fused1(m, nseq) ? forward_fused1(m, nullptr, m->d_tokens, m->cfg.max_seq_len)
+    const bool fold = use_fused1(m, nseq) && can_fold_argmax(m);
+    e = use_fused1(m, nseq) ? forward_fused1(m, nullptr, m->d_tokens, m->cfg.max_seq_len, fold)
                             : forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
-    if (!e) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
+    if (!e && !fold) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
     if (!e) {
-        hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq);
+        hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq,
+                           fold ? m->d_best : nullptr, m->d_tokens);
         if (hipGetLastError() != hipSuccess) e = JANUS_E_HIP;
     }
     hipGraph_t g = nullptr;

@@ -4,6 +4,7 @@
 // device init (:27-83), allocate_tensors' per-dtype layout choice
 // (:424-858) and the f16 packing helpers (:112-136).
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -37,26 +38,15 @@ int ensure_attn_ws(janus_ctx *ctx, size_t bytes) {
     return JANUS_OK;
 }
 
-int ensure_gemm_ws(janus_ctx *ctx, size_t bytes, size_t tiles) {
-    if (ctx->gemm_ws_bytes < bytes) {
-        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-        if (ctx->gemm_ws) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_ws));
-        ctx->gemm_ws = nullptr;
-        ctx->gemm_ws_bytes = 0;
-        size_t sz = bytes < (4u << 20) ? (4u << 20) : bytes;
-        JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->gemm_ws, sz));
-        ctx->gemm_ws_bytes = sz;
-    }
-    if (ctx->gemm_cnt_n < tiles) {
-        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-        if (ctx->gemm_cnt) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_cnt));
-        ctx->gemm_cnt = nullptr;
-        ctx->gemm_cnt_n = 0;
-        size_t n = tiles < 4096 ? 4096 : tiles;
-        JANUS_HIP_CHECK(ctx, hipMalloc((void **)&ctx->gemm_cnt, n * sizeof(uint32_t)));
-        JANUS_HIP_CHECK(ctx, hipMemset(ctx->gemm_cnt, 0, n * sizeof(uint32_t)));
-        ctx->gemm_cnt_n = n;
-    }
+int ensure_gemm_ws(janus_ctx *ctx, size_t bytes) {
+    if (ctx->gemm_ws_bytes >= bytes) return JANUS_OK;
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->gemm_ws) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_ws));
+    ctx->gemm_ws = nullptr;
+    ctx->gemm_ws_bytes = 0;
+    size_t sz = bytes < (4u << 20) ? (4u << 20) : bytes;
+    JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->gemm_ws, sz));
+    ctx->gemm_ws_bytes = sz;
     return JANUS_OK;
 }
 
@@ -245,6 +235,7 @@ int janus_create(int hip_device, janus_ctx **out) {
         return JANUS_E_HIP;
     }
     ctx->stream = ctx->own_stream;
+    if (const char *k = std::getenv("JANUS_GEMV_KERNEL")) ctx->gemv_lds = std::strcmp(k, "reg") != 0;
     *out = ctx;
     return JANUS_OK;
 }
@@ -260,7 +251,6 @@ void janus_destroy(janus_ctx *ctx) {
     if (ctx->stream && ctx->stream != ctx->own_stream) hipStreamSynchronize(ctx->stream);
     if (ctx->attn_ws) hipFree(ctx->attn_ws);
     if (ctx->gemm_ws) hipFree(ctx->gemm_ws);
-    if (ctx->gemm_cnt) hipFree(ctx->gemm_cnt);
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }

@@ -23,18 +23,18 @@
 //   F16: chunk = 16 K: the eight binary16 weights 8h..8h+7 of the chunk.
 // Padding rows and K are zero (zero scale), so they add nothing.
 //
-// Kernel: a workgroup is 4 wavefronts on 4 consecutive row groups (128 weight
-// rows) and a range of K "passes". Per pass the activations A[rows][kr]
-// (binary16) are staged in LDS once and shared by the 4 wavefronts; each
-// wavefront streams its weight chunks with 128-bit non-temporal loads,
+// Kernel: a workgroup is 16 wavefronts, 4 K slices of 4 consecutive row groups
+// (128 weight rows), over a range of K "passes". Per pass the activations
+// A[rows][kr] (binary16) are staged in LDS once and shared by all wavefronts;
+// each wavefront streams the weight chunks of its row group and K slice with 128-bit non-temporal loads,
 // unpacks them in registers into exact binary16 integers, runs
 // 32x32x16 MFMAs with fp32 accumulation per quantisation block, and applies
 // the block scale to the fp32 block result (so products and scales round
-// exactly as the M=1 kernels do). When there are too few row tiles to fill
+// exactly as the M=1 kernels do). The K slices of a row group are added in
+// slice order through LDS at the end. When there are too few row tiles to fill
 // the GPU, K is split over workgroups; the partial tiles go to a workspace
-// with agent-coherent stores and the last workgroup of each row tile (an
-// arrival counter) adds them in fixed split order, so results do not depend
-// on scheduling.
+// and a second kernel adds them in fixed split order, so results do not
+// depend on scheduling.
 #include "internal.h"
 
 namespace janus {
@@ -83,7 +83,6 @@ struct GemmArgs {
     void *c;               // output [rows][n]
     const float *resid;    // [rows][n] or null (may alias c)
     float *ws;             // split-K partials [ksplit][Mpad][Npad]
-    uint32_t *cnt;         // per row tile arrival counters (zero between launches)
     uint32_t rows, n, k;
     uint32_t chunks;       // C: chunks per row group
     uint32_t pass_chunks;  // chunks per LDS pass
@@ -239,7 +238,7 @@ struct GF16 {
     }
 };
 
-template <class F> struct Stage { static constexpr int PD = F::CK == 16 ? 16 : 8; };
+template <class F> struct Stage { static constexpr int PD = F::CK == 64 ? 4 : 8; };
 
 // Output element (m, n) of wave-tile value v for lane (32x32 MFMA C layout):
 // n = lane % 32, m = 8 * (v / 4) + 4 * (lane / 32) + v % 4.
@@ -266,47 +265,61 @@ __device__ __forceinline__ void store_tile(const GemmArgs &a, uint32_t g, int la
         }
 }
 
-template <class F, int MT>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
+// KW wavefronts per row group, each on a K slice of the pass (4 where the
+// format's registers fit 4 wavefronts per SIMD, else 2).
+template <class F, int MT, int KW>
+__global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int PD = Stage<F>::PD;
     constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
+    constexpr int SPT = 16 / KW;   // 16-byte A segments per thread per pass: Mpad * kr / 8 / (256 * KW)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rgw = wave % WAVES, kw = wave / WAVES;   // row group in the tile, K slice of the pass
     const uint32_t G = (a.n + 31) / 32;
     const uint32_t tile = blockIdx.x, ks = blockIdx.y;
-    const uint32_t g = tile * WAVES + wave;
+    const uint32_t g = tile * WAVES + rgw;
     const bool active = g < G;
     const uint32_t Mpad = MT * 32;
     _Float16 *As = (_Float16 *)smem;
     float *Ss = (float *)(smem + (size_t)Mpad * a.pitch * 2);
-    uint32_t *flag = (uint32_t *)(smem + (size_t)Mpad * a.pitch * 2 +
-                                  (SUMS ? (size_t)(a.pass_chunks * F::CK / 32) * Mpad * 4 : 0));
 
     f16x acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (f16x){};
 
+    const uint32_t cpk = a.pass_chunks / KW;   // chunks per K slice
     const uint32_t p_begin = ks * a.passes_per_wg;
     const uint32_t p_end = min(a.total_passes, p_begin + a.passes_per_wg);
     for (uint32_t p = p_begin; p < p_end; ++p) {
         const uint32_t c0 = p * a.pass_chunks, c1 = min(a.chunks, c0 + a.pass_chunks);
+        const uint32_t m0 = min(c1, c0 + kw * cpk), m1 = min(c1, m0 + cpk);   // this wave's chunks
         typename F::W wa[PD], wb[PD];
         auto load = [&](typename F::W (&w)[PD], uint32_t cs) {
 #pragma unroll
             for (int i = 0; i < PD; ++i)
-                if (cs + i < c1) w[i] = F::load(a, g, cs + i, lane);
+                if (cs + i < m1) w[i] = F::load(a, g, cs + i, lane);
         };
-        if (active) load(wa, c0);   // in flight while A is staged
+        if (active) load(wa, m0);   // in flight while A is staged
 
-        // stage A[0..Mpad)[c0*CK .. c1*CK) as binary16, zero outside rows / k
-        __syncthreads();   // the previous pass is done with LDS
+        // stage A[0..Mpad)[c0*CK .. c1*CK) as binary16, zero outside rows / k:
+        // every thread issues all of its 16-byte loads before its LDS stores
         const uint32_t kbase = c0 * F::CK, klen = (c1 - c0) * F::CK;
         const uint32_t segs_per_row = klen / 8, segs = Mpad * segs_per_row;
-        for (uint32_t s = threadIdx.x; s < segs; s += blockDim.x) {
-            const uint32_t m = s / segs_per_row, col = kbase + (s % segs_per_row) * 8;
-            uint4 v = {0u, 0u, 0u, 0u};
-            if (m < a.rows && col < a.k) v = *(const uint4 *)(a.a + (size_t)m * a.k + col);
-            *(uint4 *)(As + (size_t)m * a.pitch + (s % segs_per_row) * 8) = v;
+        uint4 sv[SPT];
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const uint32_t s = threadIdx.x + 64u * WAVES * KW * i;
+            sv[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (s < segs) {
+                const uint32_t m = s / segs_per_row, col = kbase + (s % segs_per_row) * 8;
+                if (m < a.rows && col < a.k) sv[i] = *(const uint4 *)(a.a + (size_t)m * a.k + col);
+            }
+        }
+        __syncthreads();   // the previous pass is done with LDS
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const uint32_t s = threadIdx.x + 64u * WAVES * KW * i;
+            if (s < segs) *(uint4 *)(As + (size_t)(s / segs_per_row) * a.pitch + (s % segs_per_row) * 8) = sv[i];
         }
         if (SUMS) {
             __syncthreads();
@@ -326,57 +339,65 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
         auto compute = [&](typename F::W (&w)[PD], uint32_t cs) {
 #pragma unroll
             for (int i = 0; i < PD; ++i)
-                if (cs + i < c1) F::template mma<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, Ss, 0, acc);
+                if (cs + i < m1) F::template mma<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, Ss, 0, acc);
         };
-        uint32_t cs = c0;
-        for (; cs + PD < c1; cs += 2 * PD) {
+        uint32_t cs = m0;
+        for (; cs + PD < m1; cs += 2 * PD) {
             load(wb, cs + PD);
             compute(wa, cs);
-            if (cs + 2 * PD < c1) load(wa, cs + 2 * PD);
+            if (cs + 2 * PD < m1) load(wa, cs + 2 * PD);
             compute(wb, cs + PD);
         }
-        if (cs < c1) compute(wa, cs);
+        if (cs < m1) compute(wa, cs);
     }
 
+    // add the K slices of each row group in slice order (LDS, reusing the A area)
+    if (KW > 1) {
+        float *red = (float *)smem;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[((size_t)wave * 16 + v) * 64 + lane] = acc[mt][v];
+            __syncthreads();
+            if (kw == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float sum = red[((size_t)rgw * 16 + v) * 64 + lane];
+                    for (int j = 1; j < KW; ++j) sum += red[((size_t)(j * WAVES + rgw) * 16 + v) * 64 + lane];
+                    acc[mt][v] = sum;
+                }
+            }
+        }
+    }
+    if (kw != 0 || !active) return;
     if (a.ksplit == 1) {
-        if (active) store_tile<MT>(a, g, lane, acc);
+        store_tile<MT>(a, g, lane, acc);
         return;
     }
-    // split-K: publish this split's tile, then the last workgroup of the row tile adds them in order
-    const uint32_t Npad = G * 32;
-    if (active) {
-        const uint32_t n = g * 32 + (lane & 31);
+    // split-K: this split's tile goes to the workspace; gemm_reduce_kernel adds
+    // the splits in order (the kernel boundary makes the partials visible)
+    const uint32_t Npad = G * 32, n = g * 32 + (lane & 31);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-                __hip_atomic_store(a.ws + ((size_t)ks * Mpad + out_row(mt, v, lane)) * Npad + n, acc[mt][v],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = (prev == a.ksplit - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (*flag == 0) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (active) {
-        const uint32_t n = g * 32 + (lane & 31);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float s = 0.0f;
-                for (uint32_t j = 0; j < a.ksplit; ++j)
-                    s += __hip_atomic_load(a.ws + ((size_t)j * Mpad + out_row(mt, v, lane)) * Npad + n,
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                acc[mt][v] = s;
-            }
-        store_tile<MT>(a, g, lane, acc);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int v = 0; v < 16; ++v)
+            __builtin_nontemporal_store(acc[mt][v], a.ws + ((size_t)ks * Mpad + out_row(mt, v, lane)) * Npad + n);
+}
+
+// Sums the split-K partials in split order and applies the epilogue.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, uint32_t Mpad) {
+    const uint32_t Npad = (a.n + 31) / 32 * 32;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)a.rows * a.n) return;
+    const uint32_t m = (uint32_t)(idx / a.n), n = (uint32_t)(idx % a.n);
+    const float *p = a.ws + (size_t)m * Npad + n;
+    const size_t stride = (size_t)Mpad * Npad;
+    float s = 0.0f;
+    for (uint32_t j = 0; j < a.ksplit; ++j) s += __builtin_nontemporal_load(p + j * stride);
+    if (a.resid) s += a.resid[idx];
+    if (a.c_f16) ((uint16_t *)a.c)[idx] = f2h_bits(s);
+    else ((float *)a.c)[idx] = s;
 }
 
 // ---- T32 repack (one thread per lane of a chunk) -----------------------------
@@ -537,14 +558,18 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
 
 template <class F, int MT>
 int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
+    constexpr int KW = (MT == 1 && (std::is_same<F, GQ4_0>::value || std::is_same<F, GF16>::value)) ? 4 : 2;
     const uint32_t G = (w->n + 31) / 32;
     const uint32_t tiles = (G + WAVES - 1) / WAVES;
-    const uint32_t kr = MT == 1 ? 1024 : 512;                  // K per LDS pass
+    // K per LDS pass: 1024 (M <= 32) or 512 (M <= 64); narrow products use
+    // half-size passes so that splitting K can still occupy every CU
+    uint32_t kr = MT == 1 ? 1024 : 512;
+    if (tiles * 4 < (uint32_t)ctx->num_cus && kr / F::CK >= 2 * KW) kr /= 2;
     a.pass_chunks = kr / F::CK;
     a.chunks = w->t32_chunks;
     a.total_passes = (a.chunks + a.pass_chunks - 1) / a.pass_chunks;
-    // split K over workgroups only while there are too few row tiles for ~2 per CU
-    const uint32_t want = 2u * (uint32_t)ctx->num_cus;
+    // split K over workgroups only while there are fewer row tiles than CUs
+    const uint32_t want = (uint32_t)ctx->num_cus;
     uint32_t ks = (want + tiles - 1) / tiles;
     if (ks > a.total_passes) ks = a.total_passes;
     if (ks < 1) ks = 1;
@@ -552,21 +577,28 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
     a.ksplit = (a.total_passes + a.passes_per_wg - 1) / a.passes_per_wg;
     a.pitch = a.pass_chunks * F::CK + 8;
     const bool sums = std::is_same<F, GQ4_K>::value;
-    const size_t lds = (size_t)MT * 32 * a.pitch * 2 + (sums ? (size_t)(kr / 32) * MT * 32 * 4 : 0) + 16;
+    size_t lds = (size_t)MT * 32 * a.pitch * 2 + (sums ? (size_t)(kr / 32) * MT * 32 * 4 : 0);
+    const size_t red = (size_t)WAVES * KW * 16 * 64 * 4;   // K-slice reduction, one M-tile at a time
+    if (lds < red) lds = red;
     if (a.ksplit > 1) {
         const size_t need = (size_t)a.ksplit * MT * 32 * G * 32 * 4;
-        if (int e = ensure_gemm_ws(ctx, need, tiles)) return e;
+        if (int e = ensure_gemm_ws(ctx, need)) return e;
         a.ws = (float *)ctx->gemm_ws;
-        a.cnt = ctx->gemm_cnt;
     }
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   160 * 1024);
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_mfma_kernel<F, MT>), dim3(tiles, a.ksplit), dim3(256), lds, ctx->stream, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW>), dim3(tiles, a.ksplit), dim3(64 * WAVES * KW), lds, ctx->stream, a);
     JANUS_LAUNCH_CHECK(ctx);
+    if (a.ksplit > 1) {
+        const size_t total = (size_t)a.rows * w->n;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, a,
+                           (uint32_t)(MT * 32));
+        JANUS_LAUNCH_CHECK(ctx);
+    }
     return JANUS_OK;
 }
 
