@@ -37,6 +37,7 @@ struct AttnArgs {
     uint32_t chunk;         // positions per wavefront
     uint32_t nw;            // wavefronts per workgroup
     uint32_t splits;        // S: workgroup splits per sequence
+    uint32_t qh_div;        // 0: grid.y = KV head (G query heads each); else grid.y = query head, KV head = y / qh_div
     float scale;
     int out_f16;
 };
@@ -127,7 +128,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
     constexpr int BATCH = SLOTS * U;                  // positions per batch
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = NW;
     const int slot = lane / LPP, dl = lane % LPP;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const uint32_t split = blockIdx.x, b = blockIdx.z;
+    // per-query-head launch (short contexts): one head per workgroup, KV head y / qh_div
+    const uint32_t kvh = a.qh_div ? blockIdx.y / a.qh_div : blockIdx.y;
+    const uint32_t h0 = a.qh_div ? blockIdx.y : blockIdx.y * G;   // first query head of this workgroup
     // lengths beyond the planned splits (or the capacity) are clamped, never read past
     const uint32_t span = (uint32_t)nw * a.chunk;
     const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * span);
@@ -144,7 +148,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
     float qr[G][8], acc[G][8], m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float *qp = a.q + ((size_t)b * a.heads + kvh * G + g) * D + 8 * dl;
+        const float *qp = a.q + ((size_t)b * a.heads + h0 + g) * D + 8 * dl;
         const jf4 q0 = *(const jf4 *)qp, q1 = *(const jf4 *)(qp + 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) { qr[g][i] = q0[i]; qr[g][4 + i] = q1[i]; }
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
                 for (int i = 0; i < 8; ++i) o[i] = fmaf(r[2 + 8 * dl + i], f, o[i]);
             }
         }
-        const uint32_t h = kvh * G + g;
+        const uint32_t h = h0 + g;
         if (a.splits == 1 || len <= span) {
             const float inv = 1.0f / fmaxf(L, 1e-20f);
             const size_t at = ((size_t)b * a.heads + h) * D + 8 * dl;
@@ -285,6 +289,17 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
 
 template <typename KV, int D>
 int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
+    if (a.qh_div) {   // one query head per workgroup
+        dim3 grid(a.splits, a.heads, a.batch), block(64 * a.nw);
+        const size_t lds = (size_t)a.nw * (D + 2) * 4;
+        hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 16>), grid, block, lds, ctx->stream, a);
+        JANUS_LAUNCH_CHECK(ctx);
+        if (a.splits > 1) {
+            hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+            JANUS_LAUNCH_CHECK(ctx);
+        }
+        return JANUS_OK;
+    }
     dim3 grid(a.splits, a.kv_heads, a.batch), block(64 * a.nw);
     const size_t lds = (size_t)a.nw * G * (D + 2) * 4;
     const bool big = a.nw == 16;
@@ -320,14 +335,19 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
 // wavefronts merge in LDS, so short contexts need no merge launch; otherwise
 // 4-wavefront workgroups, with a merge kernel across workgroup splits.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out) {
+                    uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out, uint32_t *qh_div_out) {
     if (max_len == 0) max_len = 1;
-    const uint64_t groups = (uint64_t)batch * kv_heads;
+    const uint32_t G = heads / kv_heads;
+    // Short contexts with few sequences: one workgroup per query head (the G
+    // heads of a KV head re-read its rows from L2) so the launch spreads over
+    // G times more CUs and each wavefront does 1/G of the arithmetic.
+    const bool qh = G > 1 && max_len <= 1024 && (uint64_t)batch * heads <= (uint64_t)ctx->num_cus;
+    *qh_div_out = qh ? G : 0;
+    const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
     const uint64_t want = (uint64_t)ctx->num_cus * 8;
     uint64_t chunk = (max_len * groups + want - 1) / want;
     chunk = (chunk + TP - 1) / TP * TP;
-    const uint32_t G = heads / kv_heads;
-    const uint32_t nw = max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4));
+    const uint32_t nw = qh ? 16 : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
     if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
     *chunk_out = (uint32_t)chunk;
     *nw_out = nw;
@@ -336,8 +356,8 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
 
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len) {
-    uint32_t chunk, nw, splits;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits);
+    uint32_t chunk, nw, splits, qh;
+    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits, &qh);
     if (splits <= 1) return JANUS_OK;
     return ensure_attn_ws(ctx, (size_t)batch * heads * splits * (hd + 2) * sizeof(float));
 }
@@ -360,10 +380,11 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.max_seq = max_seq;
     a.scale = scale;
     a.out_f16 = out_f16;
-    uint32_t chunk, nw, splits;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits);
+    uint32_t chunk, nw, splits, qh;
+    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits, &qh);
     a.chunk = chunk;
     a.nw = nw;
+    a.qh_div = qh;
     a.splits = splits;
     a.ws = nullptr;
     if (splits > 1) {

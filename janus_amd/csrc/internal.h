@@ -122,7 +122,7 @@ int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, voi
                      const int32_t *row_base, const int32_t *positions);
 // Attention split sizing shared by the launch and workspace reservation.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    uint32_t *chunk, uint32_t *nw, uint32_t *splits);
+                    uint32_t *chunk, uint32_t *nw, uint32_t *splits, uint32_t *qh_div);
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len);
 // out is f32, or binary16 when out_f16 is set.
