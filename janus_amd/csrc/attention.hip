@@ -9,7 +9,8 @@
 //    8-dimension slice), so every K/V load is a 128-bit load and a wavefront
 //    step reads SLOTS whole cache rows; scores are reduced over the slice lanes
 //    with DPP, and each slot runs an online (running max / running sum)
-//    softmax with fp32 P.V accumulators in registers. Batches of steps are
+//    softmax with fp32 P.V accumulators in registers (exponentials in base 2
+//    on log2(e)-scaled scores, one v_exp_f32 each). Batches of steps are
 //    double-buffered; there is no LDS traffic and no barrier.
 //  * Long contexts are split so the launch has ~8 wavefronts per CU; each split
 //    writes (m, l, o[D]) partials and a merge kernel combines them with the
@@ -39,6 +40,7 @@ struct AttnArgs {
     uint32_t splits;        // S: workgroup splits per sequence
     uint32_t qh_div;        // 0: grid.y = KV head (G query heads each); else grid.y = query head, KV head = y / qh_div
     float scale;
+    float scale2;           // scale * log2(e): the softmax runs in the base-2 domain
     int out_f16;
 };
 
@@ -46,6 +48,11 @@ __device__ __forceinline__ void put_out(const AttnArgs &a, size_t at, float v) {
     if (a.out_f16) ((uint16_t *)a.out)[at] = f2h_bits(v);
     else ((float *)a.out)[at] = v;
 }
+
+// 2^x with the native instruction. Scores are pre-multiplied by log2(e), so
+// exp(s - m) = 2^(s*log2e - m*log2e); all running maxima (and the partials a
+// split writes) are kept in that base-2 scale.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -101,8 +108,8 @@ __device__ __forceinline__ void merge_xor(float (&m)[G], float (&l)[G], float (&
     for (int g = 0; g < G; ++g) {
         const float mo = lane_xor<O>(m[g]), lo = lane_xor<O>(l[g]);
         const float M = fmaxf(m[g], mo);
-        const float fs = M == -INFINITY ? 0.0f : expf(m[g] - M);
-        const float fo = M == -INFINITY ? 0.0f : expf(mo - M);
+        const float fs = M == -INFINITY ? 0.0f : fexp2(m[g] - M);
+        const float fo = M == -INFINITY ? 0.0f : fexp2(mo - M);
         l[g] = l[g] * fs + lo * fo;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[g][i] = acc[g][i] * fs + lane_xor<O>(acc[g][i]) * fo;
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
                     d1 = fmaf(qr[g][i + 1], k[u].get(i + 1), d1);
                 }
                 const float t = pos_sum<LPP>(d0 + d1);
-                s[u][g] = live ? t * a.scale : -INFINITY;
+                s[u][g] = live ? t * a.scale2 : -INFINITY;
             }
         }
 #pragma unroll
@@ -192,13 +199,13 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
             for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
             const float mn = fmaxf(m[g], mx);
             if (mn == -INFINITY) continue;   // nothing live in this slot yet
-            const float alpha = expf(m[g] - mn);
+            const float alpha = fexp2(m[g] - mn);
             l[g] *= alpha;
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const float pu = expf(s[u][g] - mn);
+                const float pu = fexp2(s[u][g] - mn);
                 l[g] += pu;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pu, v[u].get(i), acc[g][i]);
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
         if (M != -INFINITY) {
             for (int w = 0; w < nw; ++w) {
                 const float *r = smem_f + ((size_t)w * G + g) * (D + 2);
-                const float f = expf(r[0] - M);
+                const float f = fexp2(r[0] - M);
                 L = fmaf(r[1], f, L);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o[i] = fmaf(r[2 + 8 * dl + i], f, o[i]);
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     float L = 0.0f, o = 0.0f;
     for (uint32_t s = 0; s < ns; ++s) {
         const float *ws = w + s * (D + 2);
-        float f = expf(ws[0] - M);
+        float f = fexp2(ws[0] - M);
         L = fmaf(ws[1], f, L);
         o = fmaf(ws[2 + threadIdx.x], f, o);
     }
@@ -379,6 +386,7 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.seq_len = seq_len;
     a.max_seq = max_seq;
     a.scale = scale;
+    a.scale2 = scale * 1.4426950408889634f;
     a.out_f16 = out_f16;
     uint32_t chunk, nw, splits, qh;
     attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits, &qh);
