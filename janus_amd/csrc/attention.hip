@@ -175,11 +175,14 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
             v[u].load(vc + (size_t)p * kvrow);
         }
     };
-    auto consume = [&](const KVRow<KV> (&k)[U], const KVRow<KV> (&v)[U], uint32_t p0) {
+    // MASK: the batch may run past `end` (only the last batch of a range);
+    // full batches skip the per-position checks.
+    auto consume = [&](const KVRow<KV> (&k)[U], const KVRow<KV> (&v)[U], uint32_t p0, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         float s[U][G];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool live = p0 + u * SLOTS + slot < end;
+            const bool live = !MASK || p0 + u * SLOTS + slot < end;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float d0 = 0.0f, d1 = 0.0f;
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
             const float mn = fmaxf(m[g], mx);
-            if (mn == -INFINITY) continue;   // nothing live in this slot yet
+            if (MASK && mn == -INFINITY) continue;   // nothing live in this slot yet
             const float alpha = fexp2(m[g] - mn);
             l[g] *= alpha;
 #pragma unroll
@@ -213,16 +216,22 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
             m[g] = mn;
         }
     };
+    const std::true_type masked{};
+    const std::false_type full{};
     if (start < end) {
         load(ka, va, start);
         uint32_t p0 = start;
         for (; p0 + BATCH < end; p0 += 2 * BATCH) {
             load(kb, vb, p0 + BATCH);
-            consume(ka, va, p0);
+            consume(ka, va, p0, full);
             if (p0 + 2 * BATCH < end) load(ka, va, p0 + 2 * BATCH);
-            consume(kb, vb, p0 + BATCH);
+            if (p0 + 2 * BATCH <= end) consume(kb, vb, p0 + BATCH, full);
+            else consume(kb, vb, p0 + BATCH, masked);
         }
-        if (p0 < end) consume(ka, va, p0);
+        if (p0 < end) {
+            if (p0 + BATCH <= end) consume(ka, va, p0, full);
+            else consume(ka, va, p0, masked);
+        }
     }
 
     // merge the slots (lanes lane ^ (LPP * 2^j) hold the same dims of other slots)
