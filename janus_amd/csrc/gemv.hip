@@ -203,22 +203,25 @@ struct FQ4_0 {
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
         const jh2 off = {(_Float16)1032.0f, (_Float16)1032.0f};
-        float s0 = 0.0f, s1 = 0.0f;
+        const jh2 off16 = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const uint32_t m = vgpr_const_6400();
+        float s0 = 0.0f, s1 = 0.0f, t0 = 0.0f, t1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t u = q[i];
-            // low nibbles: elements 4i..4i+3; high nibbles: 16+4i..16+4i+3.
-            jh2 a = as_h2((u & 0x000f000fu) | 0x64006400u) - off;          // (4i, 4i+2)
-            jh2 c = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - off;   // (4i+1, 4i+3)
-            jh2 b = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - off;   // (16+4i, 16+4i+2)
-            jh2 e = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - off;  // (16+4i+1, ..+3)
+            const uint32_t u = q[i], u8 = u >> 8;
+            // low nibbles: elements 4i..4i+3 as q - 8; high nibbles (left in
+            // place, 1024 + 16 q): 16+4i..16+4i+3 as 16 (q - 8), exact
+            jh2 a = as_h2((u & 0x000f000fu) | m) - off;        // (4i, 4i+2)
+            jh2 c = as_h2((u8 & 0x000f000fu) | m) - off;       // (4i+1, 4i+3)
+            jh2 b = as_h2((u & 0x00f000f0u) | m) - off16;      // 16 x (16+4i, 16+4i+2)
+            jh2 e = as_h2((u8 & 0x00f000f0u) | m) - off16;     // 16 x (16+4i+1, ..+3)
             // x pairs (permuted staging): v[2g] = (x[4g], x[4g+2]), v[2g+1] = (x[4g+1], x[4g+3])
             s0 = dot2(a, x.v[2 * i], s0);
             s1 = dot2(c, x.v[2 * i + 1], s1);
-            s0 = dot2(b, x.v[8 + 2 * i], s0);
-            s1 = dot2(e, x.v[8 + 2 * i + 1], s1);
+            t0 = dot2(b, x.v[8 + 2 * i], t0);
+            t1 = dot2(e, x.v[8 + 2 * i + 1], t1);
         }
-        return h2f(w.d) * (s0 + s1);
+        return h2f(w.d) * ((s0 + s1) + (t0 + t1) * 0.0625f);
     }
 };
 
@@ -261,9 +264,10 @@ struct FQ8_0 {
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            uint32_t u = q[i] ^ 0x80808080u;
-            jh2 a = as_h2((u & 0x00ff00ffu) | 0x64006400u) - off;         // (4i, 4i+2)
-            jh2 c = as_h2(((u >> 8) & 0x00ff00ffu) | 0x64006400u) - off;  // (4i+1, 4i+3)
+            // biased bytes under the 0x64 exponent byte: 1024 + (q + 128)
+            const uint32_t u = q[i] ^ 0x80808080u, c64 = 0x64646464u;
+            jh2 a = as_h2(__builtin_amdgcn_perm(u, c64, 0x00060004u)) - off;   // (4i, 4i+2)
+            jh2 c = as_h2(__builtin_amdgcn_perm(u, c64, 0x00070005u)) - off;   // (4i+1, 4i+3)
             s0 = dot2(a, x.v[2 * i], s0);
             s1 = dot2(c, x.v[2 * i + 1], s1);
         }
@@ -399,20 +403,23 @@ struct FQ4_K {
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
         const jh2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const uint32_t m = vgpr_const_6400();
         float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t u = q[i];
-            jh2 a = as_h2((u & 0x000f000fu) | 0x64006400u) - off;
-            jh2 c = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - off;
-            jh2 b = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - off;
-            jh2 e = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - off;
+            const uint32_t u = q[i], u8 = u >> 8;
+            // high nibbles stay in place: 1024 + 16 q - 1024 = 16 q exactly,
+            // so h0, h1 are 16 x the sums and scale back exactly below
+            jh2 a = as_h2((u & 0x000f000fu) | m) - off;
+            jh2 c = as_h2((u8 & 0x000f000fu) | m) - off;
+            jh2 b = as_h2((u & 0x00f000f0u) | m) - off;
+            jh2 e = as_h2((u8 & 0x00f000f0u) | m) - off;
             l0 = dot2(a, x.lo[2 * i], l0);
             l1 = dot2(c, x.lo[2 * i + 1], l1);
             h0 = dot2(b, x.hi[2 * i], h0);
             h1 = dot2(e, x.hi[2 * i + 1], h1);
         }
-        return finish(w, x, l0 + l1, h0 + h1);
+        return finish(w, x, l0 + l1, (h0 + h1) * 0.0625f);
     }
 };
 

@@ -111,6 +111,33 @@ int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weig
 bool mfma_gemm_supported(int a_dt, const janus_weight *w);
 int mfma_gemm_prepare(janus_ctx *ctx, const janus_weight *w);
 
+// Split-K partials of one MFMA product: ws[ksplit][mpad][npad] (f32).
+struct GemmPartials {
+    const float *ws;
+    uint32_t ksplit, mpad, npad;
+};
+// Batched products (binary16 rows, 1..64) whose epilogue kernel sums the
+// partials and finishes the step:
+//  gemm_qkv_rope: rows of the fused QKV weight (RoPE pairs of the q heads,
+//    of the k heads, then v) -> q rotated (f32 [rows][q_pairs * 2]), k rotated
+//    and v appended to the cache row m * max_seq + pos[m] (kv_row elements).
+//  gemm_swiglu: interleaved gate/up rows -> act (binary16 [rows][n / 2]).
+//  gemm_residual_norm: out = resid + product (f32, may alias resid), then
+//    xn = RMSNorm(out) * gamma (binary16), one workgroup per row.
+struct QkvEpilogue {
+    float *q;
+    void *kc, *vc;
+    const float *rope;
+    const int32_t *pos;
+    uint32_t q_pairs, k_pairs, half_hd, kv_row, max_seq;
+};
+int gemm_qkv_rope(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, const QkvEpilogue &e,
+                  int kv_f16);
+int gemm_swiglu(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, void *act16);
+bool resnorm_supported(uint32_t hidden);
+int gemm_residual_norm(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, const float *resid,
+                       float *out, const float *gamma, float eps, void *xn16);
+
 enum { EW_SILU = 0, EW_MUL = 1, EW_ADD = 2, EW_SWIGLU = 3 };
 int rmsnorm_launch(janus_ctx *ctx, const float *in, void *out, int out_dt, const float *gamma, uint32_t batch,
                    uint32_t hidden, float eps);
@@ -143,6 +170,15 @@ int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t 
 
 typedef _Float16 jh2 __attribute__((ext_vector_type(2)));
 typedef _Float16 jh4 __attribute__((ext_vector_type(4)));
+typedef float jf2 __attribute__((ext_vector_type(2)));
+// 0x64006400 (binary16 pair 1024, 1024) materialised in a VGPR: with the
+// constant in a register, (x & mask) | c compiles to one v_and_or_b32 (VOP3
+// takes no literal on gfx9). Not volatile, so it is hoisted and shared.
+__device__ __forceinline__ uint32_t vgpr_const_6400() {
+    uint32_t m;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
+    return m;
+}
 typedef float jf4 __attribute__((ext_vector_type(4)));
 typedef uint32_t ju4 __attribute__((ext_vector_type(4)));
 

@@ -31,6 +31,7 @@ struct janus_model {
         janus_weight *gu = nullptr;    // rows: gate_0, up_0, gate_1, up_1, ...
     };
     bool fused_ready = false;
+    bool tiles_ready = false;   // T32 tile copies of the batched products built
     std::vector<Layer> layers;
     janus_weight *tok_embd = nullptr, *lm_head = nullptr;
     float *out_norm = nullptr;
@@ -232,6 +233,61 @@ bool use_fused1(const janus_model *m, uint32_t nseq) {
     return true;
 }
 
+// The batched fused step needs binary16 activations, the fused weights of
+// every layer on the MFMA path and rows the one-workgroup norm can hold.
+bool fused_batch_ok(const janus_model *m) {
+    const janus_model_config &c = m->cfg;
+    if (c.act_dtype != JANUS_DT_F16 || c.max_batch < 2 || !m->fused_ready || !resnorm_supported(c.hidden))
+        return false;
+    for (const auto &L : m->layers)
+        if (!L.qkv || !L.gu || !mfma_gemm_supported(JANUS_DT_F16, L.qkv) || !mfma_gemm_supported(JANUS_DT_F16, L.gu) ||
+            !mfma_gemm_supported(JANUS_DT_F16, L.o) || !mfma_gemm_supported(JANUS_DT_F16, L.down))
+            return false;
+    return true;
+}
+
+bool use_fused_batch(const janus_model *m, uint32_t nseq) { return nseq > 1 && fused_batch_ok(m); }
+
+// Batched step over the fused weights: per layer the QKV product (RoPE and
+// the K/V append in its epilogue), attention, o-proj (residual add and the
+// FFN RMSNorm in its epilogue), gate/up (SwiGLU epilogue) and down-proj
+// (residual add and the next layer's attention RMSNorm, or the final norm,
+// in its epilogue). Same operations and order as forward_rows.
+int forward_batch(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t nseq, uint32_t max_len) {
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const uint32_t kvd = c.kv_heads * c.head_dim, half = c.head_dim / 2;
+    const int kv16 = c.kv_dtype == JANUS_DT_F16;
+    int e;
+    if ((e = embed_launch(ctx, m->tok_embd, h_ids, d_ids, nseq, m->hidden))) return e;
+    if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, m->layers[0].attn_norm, nseq, c.hidden, c.rms_eps)))
+        return e;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const janus_model::Layer &L = m->layers[l];
+        void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
+        const QkvEpilogue qe{m->q, kc, vc, m->rope, m->d_pos, c.heads * half, c.kv_heads * half, half, kvd,
+                             c.max_seq_len};
+        if ((e = gemm_qkv_rope(ctx, m->xn, L.qkv, nseq, qe, kv16))) return e;
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, nseq, c.heads, c.kv_heads, c.head_dim, 0,
+                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), 1)))
+            return e;
+        if ((e = gemm_residual_norm(ctx, m->attn16, L.o, nseq, m->hidden, m->h1, L.ffn_norm, c.rms_eps, m->xn)))
+            return e;
+        if ((e = gemm_swiglu(ctx, m->xn, L.gu, nseq, m->act))) return e;
+        const float *next = l + 1 < c.layers ? m->layers[l + 1].attn_norm : m->out_norm;
+        if ((e = gemm_residual_norm(ctx, m->act, L.down, nseq, m->h1, m->hidden, next, c.rms_eps, m->xn))) return e;
+    }
+    return gemm_dispatch(ctx, m->xn, JANUS_DT_F16, m->lm_head, m->logits, JANUS_DT_F32, nseq, nullptr);
+}
+
+int forward_any(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t nseq, uint32_t max_len,
+                bool fold_argmax) {
+    if (use_fused1(m, nseq)) return forward_fused1(m, h_ids, d_ids, max_len, fold_argmax);
+    if (use_fused_batch(m, nseq)) return forward_batch(m, h_ids, d_ids, nseq, max_len);
+    return forward_rows(m, h_ids, d_ids, nseq, max_len);
+}
+
 struct Positions {
     int32_t p[64];
 };
@@ -363,6 +419,7 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
     };
     free_graph(m);
     m->fused_ready = false;
+    m->tiles_ready = false;
     for (auto &L : m->layers) {
         janus_weight_free(ctx, L.qkv);
         janus_weight_free(ctx, L.gu);
@@ -407,16 +464,25 @@ int janus_model_validate(janus_model *m) {
             return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
     }
     if (m->cfg.act_dtype != JANUS_DT_F16) return JANUS_OK;
-    if (m->cfg.max_batch > 1) {
-        // tile copies for the batched MFMA products, built before any graph capture
-        for (auto &L : m->layers)
-            for (const janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+    if (int e = ensure_fused(m)) return e;
+    if (m->cfg.max_batch > 1 && !m->tiles_ready) {
+        // tile copies for the batched MFMA products, built before any graph
+        // capture: the fused QKV and gate/up weights where the fused batched
+        // step runs, the separate ones otherwise
+        const bool fb = fused_batch_ok(m);
+        for (auto &L : m->layers) {
+            std::vector<const janus_weight *> ws{L.o, L.down};
+            if (fb) ws.insert(ws.end(), {L.qkv, L.gu});
+            else ws.insert(ws.end(), {L.q, L.k, L.v, L.gate, L.up});
+            for (const janus_weight *w : ws)
                 if (mfma_gemm_supported(JANUS_DT_F16, w))
                     if (int e = mfma_gemm_prepare(m->ctx, w)) return e;
+        }
         if (mfma_gemm_supported(JANUS_DT_F16, m->lm_head))
             if (int e = mfma_gemm_prepare(m->ctx, m->lm_head)) return e;
+        m->tiles_ready = true;
     }
-    return ensure_fused(m);
+    return JANUS_OK;
 }
 
 int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_each) {
@@ -459,8 +525,7 @@ int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *
         max_len = positions[i] + 1 > max_len ? positions[i] + 1 : max_len;
     }
     if (int e = upload_positions(m, positions, nseq)) return e;
-    if (use_fused1(m, nseq)) return forward_fused1(m, tokens, nullptr, max_len);
-    return forward_rows(m, tokens, nullptr, nseq, max_len);
+    return forward_any(m, tokens, nullptr, nseq, max_len, false);
 }
 
 const float *janus_model_logits(const janus_model *m) { return m ? m->logits : nullptr; }
@@ -540,8 +605,7 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
         return hip_fail(ctx, be, "hipStreamBeginCapture");
     }
     const bool fold = use_fused1(m, nseq) && can_fold_argmax(m);
-    e = use_fused1(m, nseq) ? forward_fused1(m, nullptr, m->d_tokens, m->cfg.max_seq_len, fold)
-                            : forward_rows(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len);
+    e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, fold);
     if (!e && !fold) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
     if (!e) {
         hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq,

@@ -48,12 +48,21 @@ constexpr int WAVES = 4;   // row groups per workgroup
 __device__ __forceinline__ jh2 as_h2(uint32_t u) { return __builtin_bit_cast(jh2, u); }
 
 // 8 permuted nibbles -> 8 binary16 (1024 + q) - off, natural element order.
+// Slots 0/4 and 2/6 (mask 0x000f000f) become 1024 + q; slots 1/5 and 3/7
+// (mask 0x00f000f0) become 1024 + 16 q, scaled back exactly by one FMA
+// ((1024 + 16 q) / 16 - 64 - (off - 1024) = q - (off - 1024)). The magic
+// exponent sits in a VGPR so each mask-and-merge is one v_and_or_b32.
 __device__ __forceinline__ h8 unpack_nib8(uint32_t u, _Float16 off) {
     const jh2 o = {off, off};
-    jh2 p0 = as_h2((u & 0x000f000fu) | 0x64006400u) - o;
-    jh2 p1 = as_h2(((u >> 4) & 0x000f000fu) | 0x64006400u) - o;
-    jh2 p2 = as_h2(((u >> 8) & 0x000f000fu) | 0x64006400u) - o;
-    jh2 p3 = as_h2(((u >> 12) & 0x000f000fu) | 0x64006400u) - o;
+    const jh2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const _Float16 cb = (_Float16)(960.0f - (float)off);
+    const jh2 c = {cb, cb};
+    const uint32_t m = vgpr_const_6400();
+    const uint32_t u8 = u >> 8;
+    const jh2 p0 = as_h2((u & 0x000f000fu) | m) - o;
+    const jh2 p1 = __builtin_elementwise_fma(as_h2((u & 0x00f000f0u) | m), s16, c);
+    const jh2 p2 = as_h2((u8 & 0x000f000fu) | m) - o;
+    const jh2 p3 = __builtin_elementwise_fma(as_h2((u8 & 0x00f000f0u) | m), s16, c);
     return (h8){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
@@ -91,6 +100,7 @@ struct GemmArgs {
     uint32_t ksplit;
     uint32_t pitch;        // LDS row pitch of A, in halves
     int c_f16;
+    int to_ws;             // write partials to ws even when ksplit == 1 (epilogue kernels read them)
 };
 
 // ---- formats ------------------------------------------------------------------
@@ -267,12 +277,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs &a, uint32_t g, int la
 
 // KW wavefronts per row group, each on a K slice of the pass (4 where the
 // format's registers fit 4 wavefronts per SIMD, else 2).
-template <class F, int MT, int KW>
+// SPT: 16-byte A segments per thread per pass, Mpad * kr / 8 / (256 * KW).
+template <class F, int MT, int KW, int SPT, int PD = Stage<F>::PD>
 __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int PD = Stage<F>::PD;
     constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
-    constexpr int SPT = 16 / KW;   // 16-byte A segments per thread per pass: Mpad * kr / 8 / (256 * KW)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rgw = wave % WAVES, kw = wave / WAVES;   // row group in the tile, K slice of the pass
     const uint32_t G = (a.n + 31) / 32;
@@ -371,7 +380,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
         }
     }
     if (kw != 0 || !active) return;
-    if (a.ksplit == 1) {
+    if (a.ksplit == 1 && !a.to_ws) {
         store_tile<MT>(a, g, lane, acc);
         return;
     }
@@ -557,20 +566,30 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
 }
 
 template <class F, int MT>
-int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
-    constexpr int KW = (MT == 1 && (std::is_same<F, GQ4_0>::value || std::is_same<F, GF16>::value)) ? 4 : 2;
+constexpr int gemm_kw() {
+    return (MT == 1 && (std::is_same<F, GQ4_0>::value || std::is_same<F, GF16>::value)) ? 4 : 2;
+}
+
+// kr_force / ks_force (0 = automatic) fix the pass length and the K split.
+template <class F, int MT, int KW = gemm_kw<F, MT>(), int PD = Stage<F>::PD>
+int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials *parts, uint32_t kr_force = 0,
+                uint32_t ks_force = 0) {
+    constexpr int SPT1 = 16 / KW;   // kr = 1024 / MT
     const uint32_t G = (w->n + 31) / 32;
     const uint32_t tiles = (G + WAVES - 1) / WAVES;
     // K per LDS pass: 1024 (M <= 32) or 512 (M <= 64); narrow products use
     // half-size passes so that splitting K can still occupy every CU
     uint32_t kr = MT == 1 ? 1024 : 512;
     if (tiles * 4 < (uint32_t)ctx->num_cus && kr / F::CK >= 2 * KW) kr /= 2;
+    if (kr_force) kr = kr_force;
+    if (kr % (F::CK * KW) || kr * MT > 2048) return fail(ctx, JANUS_E_INVALID_DIM, "gemm: bad pass length");
     a.pass_chunks = kr / F::CK;
     a.chunks = w->t32_chunks;
     a.total_passes = (a.chunks + a.pass_chunks - 1) / a.pass_chunks;
     // split K over workgroups only while there are fewer row tiles than CUs
     const uint32_t want = (uint32_t)ctx->num_cus;
     uint32_t ks = (want + tiles - 1) / tiles;
+    if (ks_force) ks = ks_force;
     if (ks > a.total_passes) ks = a.total_passes;
     if (ks < 1) ks = 1;
     a.passes_per_wg = (a.total_passes + ks - 1) / ks;
@@ -580,19 +599,31 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
     size_t lds = (size_t)MT * 32 * a.pitch * 2 + (sums ? (size_t)(kr / 32) * MT * 32 * 4 : 0);
     const size_t red = (size_t)WAVES * KW * 16 * 64 * 4;   // K-slice reduction, one M-tile at a time
     if (lds < red) lds = red;
-    if (a.ksplit > 1) {
+    a.to_ws = parts != nullptr;
+    if (a.ksplit > 1 || parts) {
         const size_t need = (size_t)a.ksplit * MT * 32 * G * 32 * 4;
         if (int e = ensure_gemm_ws(ctx, need)) return e;
         a.ws = (float *)ctx->gemm_ws;
     }
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024);
+        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW, SPT1, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW, 2 * SPT1, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW>), dim3(tiles, a.ksplit), dim3(64 * WAVES * KW), lds, ctx->stream, a);
+    const dim3 grid(tiles, a.ksplit), block(64 * WAVES * KW);
+    if (kr * MT <= 1024) hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, SPT1, PD>), grid, block, lds, ctx->stream, a);
+    else hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, 2 * SPT1, PD>), grid, block, lds, ctx->stream, a);
     JANUS_LAUNCH_CHECK(ctx);
+    if (parts) {
+        parts->ws = a.ws;
+        parts->ksplit = a.ksplit;
+        parts->mpad = MT * 32;
+        parts->npad = G * 32;
+        return JANUS_OK;
+    }
     if (a.ksplit > 1) {
         const size_t total = (size_t)a.rows * w->n;
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, a,
@@ -603,13 +634,150 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w) {
 }
 
 template <int MT>
-int launch_mt(janus_ctx *ctx, const GemmArgs &a, const janus_weight *w) {
+int launch_mt(janus_ctx *ctx, const GemmArgs &a, const janus_weight *w, GemmPartials *parts) {
     switch (w->type) {
-    case JANUS_DT_Q4_0: return launch_mfma<GQ4_0, MT>(ctx, a, w);
-    case JANUS_DT_Q8_0: return launch_mfma<GQ8_0, MT>(ctx, a, w);
-    case JANUS_DT_Q4_K: return launch_mfma<GQ4_K, MT>(ctx, a, w);
-    default: return launch_mfma<GF16, MT>(ctx, a, w);
+    case JANUS_DT_Q4_0: return launch_mfma<GQ4_0, MT>(ctx, a, w, parts);
+    case JANUS_DT_Q8_0: return launch_mfma<GQ8_0, MT>(ctx, a, w, parts);
+    case JANUS_DT_Q4_K: return launch_mfma<GQ4_K, MT>(ctx, a, w, parts);
+    default: return launch_mfma<GF16, MT>(ctx, a, w, parts);
     }
+}
+
+GemmArgs make_args(const janus_weight *w, const void *a, void *c, int c_f16, uint32_t rows, const float *residual) {
+    GemmArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.qs = w->t32_qs;
+    g.side = w->t32_side;
+    g.a = (const _Float16 *)a;
+    g.c = c;
+    g.resid = residual;
+    g.rows = rows;
+    g.n = w->n;
+    g.k = w->k;
+    g.c_f16 = c_f16;
+    return g;
+}
+
+// ---- batched epilogues over the split-K partials ------------------------------
+// Each sums the splits of an element in split order, like gemm_reduce_kernel;
+// the loads of up to 8 splits are issued together.
+
+template <typename V>
+__device__ __forceinline__ V sum_splits(const float *q, size_t stride, uint32_t ksplit) {
+    V s = {};
+    for (uint32_t k0 = 0; k0 < ksplit; k0 += 8) {
+        V u[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            if (k0 + kk < ksplit) u[kk] = __builtin_nontemporal_load((const V *)(q + (k0 + kk) * stride));
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            if (k0 + kk < ksplit) s += u[kk];
+    }
+    return s;
+}
+
+__device__ __forceinline__ jf2 sum_pair(const GemmPartials &p, uint32_t m, uint32_t col) {
+    return sum_splits<jf2>(p.ws + (size_t)m * p.npad + col, (size_t)p.mpad * p.npad, p.ksplit);
+}
+
+// Fused-QKV rows (RoPE pairs of q heads, of k heads, then v in order): rotate
+// q into q_out [rows][heads * hd] (f32) and k, append k and v to the cache row
+// m * max_seq + pos[m] (the rotation of rope.wgsl:71-72, the row layout of
+// kv_update_kernel).
+template <typename KV>
+__global__ __launch_bounds__(256) void epi_qkv_rope_kernel(GemmPartials p, QkvEpilogue e, uint32_t rows) {
+    const uint32_t pairs = e.q_pairs + e.k_pairs + e.kv_row / 2;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)rows * pairs) return;
+    const uint32_t m = (uint32_t)(idx / pairs), g = (uint32_t)(idx % pairs);
+    const uint32_t pos = (uint32_t)e.pos[m];
+    if (pos >= e.max_seq) return;   // host checks keep positions in range; never index past the tables
+    const jf2 r = sum_pair(p, m, 2 * g);
+    const size_t row = (size_t)m * e.max_seq + pos;
+    if (g < e.q_pairs + e.k_pairs) {
+        const bool isq = g < e.q_pairs;
+        const uint32_t gg = isq ? g : g - e.q_pairs, h = gg / e.half_hd, i = gg % e.half_hd;
+        const float2 cs = *(const float2 *)(e.rope + 2 * ((size_t)pos * e.half_hd + i));
+        const float y0 = r.x * cs.x - r.y * cs.y;
+        const float y1 = r.x * cs.y + r.y * cs.x;
+        if (isq) {
+            float *q = e.q + (size_t)m * e.q_pairs * 2 + (size_t)h * 2 * e.half_hd + i;
+            q[0] = y0;
+            q[e.half_hd] = y1;
+        } else {
+            KV *k = (KV *)e.kc + row * e.kv_row + (size_t)h * 2 * e.half_hd + i;
+            k[0] = (KV)y0;
+            k[e.half_hd] = (KV)y1;
+        }
+    } else {
+        KV *v = (KV *)e.vc + row * e.kv_row + 2 * (size_t)(g - e.q_pairs - e.k_pairs);
+        v[0] = (KV)r.x;
+        v[1] = (KV)r.y;
+    }
+}
+
+// Gate/up rows interleaved (gate_j, up_j): act[m][j] = silu(gate) * up as
+// binary16 (the SwiGLU of elementwise_kernel).
+__global__ __launch_bounds__(256) void epi_swiglu_kernel(GemmPartials p, _Float16 *act, uint32_t rows, uint32_t ffn) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)rows * ffn) return;
+    const uint32_t m = (uint32_t)(idx / ffn), j = (uint32_t)(idx % ffn);
+    const jf2 r = sum_pair(p, m, 2 * j);
+    const float v = r.x * (1.0f / (1.0f + expf(-r.x))) * r.y;
+    ((uint16_t *)act)[idx] = f2h_bits(v);
+}
+
+// One 1024-thread workgroup per row: out[m] = resid[m] + product (f32, may
+// alias resid), then xn[m] = (out[m] / rms) * gamma as binary16 with
+// rms = sqrt(mean(out^2) + eps) (the arithmetic of rmsnorm_kernel).
+template <int NV>
+__global__ __launch_bounds__(1024) void epi_resnorm_kernel(GemmPartials p, const float *resid, float *out,
+                                                           const float *__restrict__ gamma, float eps, _Float16 *xn,
+                                                           uint32_t hidden) {
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x;
+    const float *q = p.ws + (size_t)m * p.npad;
+    const size_t stride = (size_t)p.mpad * p.npad;
+    jf4 v[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = 4 * (threadIdx.x + 1024u * j);
+        v[j] = jf4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (i < hidden) v[j] = sum_splits<jf4>(q + i, stride, p.ksplit) + *(const jf4 *)(resid + (size_t)m * hidden + i);
+        s = fmaf(v[j].x, v[j].x, s);
+        s = fmaf(v[j].y, v[j].y, s);
+        s = fmaf(v[j].z, v[j].z, s);
+        s = fmaf(v[j].w, v[j].w, s);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) tot += red[w];
+    const float rms = sqrtf(tot / (float)hidden + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = 4 * (threadIdx.x + 1024u * j);
+        if (i < hidden) {
+            *(jf4 *)(out + (size_t)m * hidden + i) = v[j];
+            const jf4 g = *(const jf4 *)(gamma + i);
+            const uint32_t lo = (uint32_t)f2h_bits((v[j].x / rms) * g.x) | ((uint32_t)f2h_bits((v[j].y / rms) * g.y) << 16);
+            const uint32_t hi = (uint32_t)f2h_bits((v[j].z / rms) * g.z) | ((uint32_t)f2h_bits((v[j].w / rms) * g.w) << 16);
+            *(uint2 *)((uint16_t *)xn + (size_t)m * hidden + i) = make_uint2(lo, hi);
+        }
+    }
+}
+
+int run_partials(janus_ctx *ctx, const void *a, const janus_weight *w, uint32_t rows, GemmPartials *parts) {
+    if (!mfma_gemm_supported(JANUS_DT_F16, w))
+        return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "batched epilogue: weight has no MFMA path");
+    if (rows == 0 || rows > 64) return fail(ctx, JANUS_E_INVALID_DIM, "batched epilogue: rows must be 1..64");
+    if (int e = mfma_gemm_prepare(ctx, w)) return e;
+    const GemmArgs g = make_args(w, a, nullptr, 0, rows, nullptr);
+    return rows <= 32 ? launch_mt<1>(ctx, g, w, parts) : launch_mt<2>(ctx, g, w, parts);
 }
 
 }  // namespace
@@ -628,18 +796,8 @@ int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weig
                        uint32_t rows, const float *residual) {
     if (mfma_gemm_supported(a_dt, w)) {
         if (int e = mfma_gemm_prepare(ctx, w)) return e;
-        GemmArgs g;
-        std::memset(&g, 0, sizeof(g));
-        g.qs = w->t32_qs;
-        g.side = w->t32_side;
-        g.a = (const _Float16 *)a;
-        g.c = c;
-        g.resid = residual;
-        g.rows = rows;
-        g.n = w->n;
-        g.k = w->k;
-        g.c_f16 = c_dt == JANUS_DT_F16;
-        return rows <= 32 ? launch_mt<1>(ctx, g, w) : launch_mt<2>(ctx, g, w);
+        const GemmArgs g = make_args(w, a, c, c_dt == JANUS_DT_F16, rows, residual);
+        return rows <= 32 ? launch_mt<1>(ctx, g, w, nullptr) : launch_mt<2>(ctx, g, w, nullptr);
     }
     // f32 activations keep the reference's dtype: one GEMV launch per row
     const size_t as = act_bytes(a_dt) * w->k, cs = act_bytes(c_dt) * w->n;
@@ -648,6 +806,48 @@ int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weig
                               residual ? residual + (size_t)r * w->n : nullptr);
         if (e) return e;
     }
+    return JANUS_OK;
+}
+
+int gemm_qkv_rope(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, const QkvEpilogue &e,
+                  int kv_f16) {
+    if (w->n != 2 * (e.q_pairs + e.k_pairs) + e.kv_row || e.kv_row % 2)
+        return fail(ctx, JANUS_E_INVALID_DIM, "qkv epilogue: row count does not match the head layout");
+    GemmPartials p{};
+    if (int r = run_partials(ctx, a16, w, rows, &p)) return r;
+    const size_t total = (size_t)rows * (w->n / 2);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (kv_f16) hipLaunchKernelGGL(epi_qkv_rope_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, p, e, rows);
+    else hipLaunchKernelGGL(epi_qkv_rope_kernel<float>, grid, dim3(256), 0, ctx->stream, p, e, rows);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+int gemm_swiglu(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, void *act16) {
+    if (w->n % 2) return fail(ctx, JANUS_E_INVALID_DIM, "swiglu epilogue: odd row count");
+    GemmPartials p{};
+    if (int r = run_partials(ctx, a16, w, rows, &p)) return r;
+    const size_t total = (size_t)rows * (w->n / 2);
+    hipLaunchKernelGGL(epi_swiglu_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, p,
+                       (_Float16 *)act16, rows, w->n / 2);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+bool resnorm_supported(uint32_t hidden) { return hidden % 4 == 0 && hidden <= 8192; }
+
+int gemm_residual_norm(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, const float *resid,
+                       float *out, const float *gamma, float eps, void *xn16) {
+    const uint32_t hidden = w->n;
+    if (!resnorm_supported(hidden))
+        return fail(ctx, JANUS_E_INVALID_DIM, "residual-norm epilogue: rows must be a multiple of 4, at most 8192");
+    GemmPartials p{};
+    if (int r = run_partials(ctx, a16, w, rows, &p)) return r;
+    const dim3 grid(rows), block(1024);
+    _Float16 *xn = (_Float16 *)xn16;
+    if (hidden <= 4096) hipLaunchKernelGGL(epi_resnorm_kernel<1>, grid, block, 0, ctx->stream, p, resid, out, gamma, eps, xn, hidden);
+    else hipLaunchKernelGGL(epi_resnorm_kernel<2>, grid, block, 0, ctx->stream, p, resid, out, gamma, eps, xn, hidden);
+    JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
 }
 

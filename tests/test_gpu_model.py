@@ -173,29 +173,64 @@ def test_fused_graph_matches_fused_eager(engine):
     assert outs[0] == outs[1]
 
 
-@pytest.mark.parametrize("qtype", [synth.Q4_0, synth.Q4_K])
-def test_batched_f16_path_equals_single_sequences(engine, qtype):
-    """Ragged batch with binary16 activations (MFMA GEMM, per-sequence positions)
-    against each sequence run alone on the fused single-sequence GEMV path."""
+@pytest.mark.parametrize("qtype,kv_dtype", [(synth.Q4_0, _lib.DT_F16), (synth.Q4_K, _lib.DT_F16),
+                                             (synth.Q8_0, _lib.DT_F32)])
+def test_batched_f16_path_equals_single_sequences(engine, qtype, kv_dtype):
+    """Ragged batch with binary16 activations (fused batched step: MFMA
+    products with RoPE/KV-append, residual+RMSNorm and SwiGLU epilogues,
+    per-sequence positions) against each sequence run alone on the fused
+    single-sequence GEMV path, and against the oracle."""
     spec = _mini_llama3(17, qtype)
     rng = np.random.default_rng(19)
     lens = [5, 12, 8]
     prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
     singles = []
     for pr in prompts:
-        m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        m = Model(engine, spec, max_seq_len=32, kv_dtype=kv_dtype, act_dtype=_lib.DT_F16)
         for p, t in enumerate(pr):
             m.forward([t], [p])
         singles.append(m.logits()[0])
         m.close()
-    mb = Model(engine, spec, max_seq_len=32, max_batch=3, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    mb = Model(engine, spec, max_seq_len=32, max_batch=3, kv_dtype=kv_dtype, act_dtype=_lib.DT_F16)
     for step in range(max(lens)):
         mb.forward([pr[min(step, len(pr) - 1)] for pr in prompts], [min(step, len(pr) - 1) for pr in prompts])
     out = mb.logits(3)
     for s in range(3):
         assert _rel_err(out[s], singles[s]) <= 1e-3
-    ref = O.OracleModel(spec, 32, kv_f16=True)
+    ref = O.OracleModel(spec, 32, kv_f16=(kv_dtype == _lib.DT_F16))
     for p, t in enumerate(prompts[1]):
         want = ref.forward(t, p)
     assert _rel_err(out[1], want) <= REL
     mb.close()
+
+
+def test_batched_graph_matches_batched_eager(engine):
+    """Graph replays of the fused batched step (device positions, in-graph
+    argmax) give the token streams of eager batched steps."""
+    spec = _mini_llama3(23)
+    rng = np.random.default_rng(29)
+    lens = [6, 3, 9, 4]
+    prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
+    outs = []
+    for use_graph in (False, True):
+        m = Model(engine, spec, max_seq_len=48, max_batch=4, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for step in range(max(lens)):
+            m.forward([pr[min(step, len(pr) - 1)] for pr in prompts], [min(step, len(pr) - 1) for pr in prompts])
+        last = [pr[-1] for pr in prompts]
+        pos = [len(pr) for pr in prompts]
+        toks = []
+        if use_graph:
+            m.graph_begin(last, pos)
+            for _ in range(10):
+                m.graph_run(1)
+                toks.append(m.graph_tokens(4))
+        else:
+            for _ in range(10):
+                m.forward(last, pos)
+                logits = m.logits(4)
+                last = [O.argmax_last(logits[s]) for s in range(4)]
+                toks.append(list(last))
+                pos = [p + 1 for p in pos]
+        outs.append([list(map(int, t)) for t in toks])
+        m.close()
+    assert outs[0] == outs[1]
