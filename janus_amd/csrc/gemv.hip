@@ -37,6 +37,7 @@ namespace {
 #endif
 
 constexpr int XB = 32;                 // activation elements per LDS block
+constexpr int NORM_MAXG = 1;           // normalised LDS staging: k <= 16 * 512 * NORM_MAXG
 template <typename XT> struct XLayout;
 template <> struct XLayout<float> {    // 32 floats + 4 pad = 144 B
     static constexpr int STRIDE = 36;
@@ -819,6 +820,82 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
     else gemv_reg_body<F, XT, BPL, R, false>(a);
 }
 
+// Rounds 16 staged values (group g of x) to binary16, writes them to LDS in
+// the layout of stage_x and their sum to sx16[g].
+template <bool PERM>
+__device__ __forceinline__ void store_x16(const float (&v)[16], uint32_t g, _Float16 *xs, float *sx16) {
+    const uint32_t e0 = g * 16;
+    _Float16 hv[16];
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        hv[t] = (_Float16)v[t];
+        s += (float)hv[t];
+    }
+    sx16[g] = s;
+    _Float16 *dst = xs + (e0 / 32) * XLayout<_Float16>::STRIDE + (e0 % 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const jh4 o = PERM ? (jh4){hv[4 * q], hv[4 * q + 2], hv[4 * q + 1], hv[4 * q + 3]}
+                           : (jh4){hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+        *(jh4 *)(dst + 4 * q) = o;
+    }
+}
+
+// RMS-normalised staging of f32 x (512-thread workgroups, k <= 16 * 512 * MAXG):
+// every thread loads its 16-element groups once, with all loads in flight
+// together; the sum of squares is reduced over the workgroup in a fixed order
+// (thread order, then wavefront order), then x / rms * gamma is staged.
+template <bool PERM, int MAXG>
+__device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16 *xs, float *sx16,
+                               const float *__restrict__ gamma, float eps, float *red) {
+    const uint32_t g16 = (k + 15) / 16;
+    float v[MAXG][16];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXG; ++j) {
+        const uint32_t g = threadIdx.x + 512u * j, e0 = g * 16;
+        if (e0 + 16 <= k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const jf4 xa = *(const jf4 *)(x + e0 + 4 * q);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[j][4 * q + t] = xa[t];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) v[j][t] = e0 + t < k ? x[e0 + t] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXG; ++j)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) ss = fmaf(v[j][t], v[j][t], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += red[w];
+    const float rms = sqrtf(tot / (float)k + eps);
+#pragma unroll
+    for (int j = 0; j < MAXG; ++j) {
+        const uint32_t g = threadIdx.x + 512u * j, e0 = g * 16;
+        if (g >= g16) continue;
+        if (e0 + 16 <= k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const jf4 ga = *(const jf4 *)(gamma + e0 + 4 * q);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[j][4 * q + t] = (v[j][4 * q + t] / rms) * ga[t];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) v[j][t] = e0 + t < k ? (v[j][t] / rms) * gamma[e0 + t] : 0.0f;
+        }
+        store_x16<PERM>(v[j], g, xs, sx16);
+    }
+}
+
 // Vectorised staging of binary16 x for the LDS kernel: each thread handles
 // groups of 16 elements (16-byte global loads of x, and of gamma when
 // normalising) and writes them with 8-byte LDS stores in the layout of
@@ -858,21 +935,7 @@ __device__ void stage_x16(const void *__restrict__ xin, uint32_t k, _Float16 *xs
                 for (int t = 0; t < 16; ++t) v[t] = e0 + t < k ? (float)x[e0 + t] : 0.0f;
             }
         }
-        _Float16 hv[16];
-        float s = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            hv[t] = (_Float16)v[t];
-            s += (float)hv[t];
-        }
-        sx16[g] = s;
-        _Float16 *dst = xs + (e0 / 32) * XLayout<_Float16>::STRIDE + (e0 % 32);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const jh4 o = PERM ? (jh4){hv[4 * q], hv[4 * q + 2], hv[4 * q + 1], hv[4 * q + 3]}
-                               : (jh4){hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
-            *(jh4 *)(dst + 4 * q) = o;
-        }
+        store_x16<PERM>(v, g, xs, sx16);
     }
 }
 
@@ -890,16 +953,7 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
     float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
     auto stage = [&]() {
         if constexpr (NORM) {
-            const float *x = (const float *)a.x;
-            float ss = 0.0f;
-            for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-            ss = wave_sum(ss);
-            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-            __syncthreads();
-            float tot = 0.0f;
-            for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += red[w];
-            const float rms = sqrtf(tot / (float)a.k + a.eps);
-            stage_x16<F::PERM, true>(x, a.k, xs, sx16, a.gamma, rms);
+            stage_x16_norm<F::PERM, NORM_MAXG>((const float *)a.x, a.k, xs, sx16, a.gamma, a.eps, red);
         } else {
             stage_x16<F::PERM, false>(a.x, a.k, xs, sx16, nullptr, 1.0f);
         }
@@ -1138,6 +1192,7 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
     const bool norm = gamma != nullptr;
     bool done = false;
     int e = JANUS_OK;
+    if (norm && w->k > 16u * 512u * NORM_MAXG) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: normalised row too long");
     switch (w->type) {
     case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, norm, true, done); break;
     case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, norm, true, done); break;
@@ -1169,6 +1224,7 @@ int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float
     a.eps = eps;
     bool done = false;
     int e = JANUS_OK;
+    if (w->k > 16u * 512u * NORM_MAXG) return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: row too long");
     switch (w->type) {
     case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, true, false, done); break;
     case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, true, false, done); break;

@@ -227,7 +227,8 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
 bool can_fold_argmax(const janus_model *m) { return can_fold_head(m); }
 
 bool use_fused1(const janus_model *m, uint32_t nseq) {
-    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready) return false;
+    // the fused norms stage x in registers: hidden <= 8192
+    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready || m->cfg.hidden > 8192) return false;
     for (const auto &L : m->layers)
         if (!L.qkv || !L.gu) return false;
     return true;
