@@ -72,6 +72,68 @@ def decode_bs1(engine, spec, steps: int, warmup: int, prompt_len: int = 128):
     return ms, toks
 
 
+L2 = dict(hidden=4096, heads=32, kv_heads=32, ffn=11008, vocab=32000, layers=32, rope_theta=10000.0)
+
+
+def llama2_q4k_spec(seed: int, layers: int = 32):
+    """BASELINE config 3 architecture (Llama-2-7B: 32 layers, hidden 4096, 32 MHA
+    heads, FFN 11008, vocab 32000) with Q4_K blocks quantised from N(0, 0.02).
+    Quantising 6.7 B weights in numpy takes minutes, so one 4096x4096, one
+    11008x4096 and one 4096x11008 matrix are quantised and their bytes reused
+    for every layer's q/k/v/o, gate/up and down (each layer is still uploaded
+    and streamed from HBM separately); norms and embeddings are per layer."""
+    from janus_amd import synth
+    rng = np.random.default_rng(seed)
+    h, f, v = L2["hidden"], L2["ffn"], L2["vocab"]
+    sq = synth.Tensor("", synth.Q4_K, h, h, synth.random_q4_k(rng, h, h))
+    gu = synth.Tensor("", synth.Q4_K, f, h, synth.random_q4_k(rng, f, h))
+    dn = synth.Tensor("", synth.Q4_K, h, f, synth.random_q4_k(rng, h, f))
+    spec = synth.ModelSpec(h, L2["heads"], L2["kv_heads"], f, v, layers, 1e-5, L2["rope_theta"])
+    spec.tensors.append(synth.Tensor("token_embd.weight", synth.F16, v, h,
+                                     synth.f16_bits(rng.standard_normal((v, h), dtype=np.float32))))
+    norm = lambda: 1 + rng.standard_normal(h, dtype=np.float32) * np.float32(0.02)
+    for l in range(layers):
+        p = f"blk.{l}."
+        spec.tensors.append(synth.Tensor(p + "attn_norm.weight", synth.F32, h, 0, norm()))
+        for name in ("attn_q", "attn_k", "attn_v", "attn_output"):
+            spec.tensors.append(synth.Tensor(p + name + ".weight", synth.Q4_K, h, h, sq.data))
+        spec.tensors.append(synth.Tensor(p + "ffn_norm.weight", synth.F32, h, 0, norm()))
+        spec.tensors.append(synth.Tensor(p + "ffn_gate.weight", synth.Q4_K, f, h, gu.data))
+        spec.tensors.append(synth.Tensor(p + "ffn_up.weight", synth.Q4_K, f, h, gu.data))
+        spec.tensors.append(synth.Tensor(p + "ffn_down.weight", synth.Q4_K, h, f, dn.data))
+    spec.tensors.append(synth.Tensor("output_norm.weight", synth.F32, h, 0, norm()))
+    spec.tensors.append(synth.Tensor("output.weight", synth.F16, v, h,
+                                     synth.f16_bits(rng.standard_normal((v, h), dtype=np.float32) * np.float32(0.02))))
+    return spec
+
+
+def decode_c3(engine, spec, prompt_len: int = 512, ctx: int = 2048):
+    """BASELINE config 3 workload: a 512-token random-id prompt prefilled token
+    by token, then greedy decode to a 2048-token context (HIP-graph steps), fp16
+    KV, batch 1. Returns (decode ms total, decode tokens, prefill s)."""
+    import torch
+    from janus_amd import _lib
+    from janus_amd.model import Model
+    m = Model(engine, spec, max_seq_len=ctx, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    prompt = np.random.default_rng(3).integers(0, spec.vocab, prompt_len).tolist()
+    t0 = time.perf_counter()
+    for p, t in enumerate(prompt):
+        m.forward([t], [p])
+    engine.sync()
+    prefill_s = time.perf_counter() - t0
+    steps = ctx - prompt_len
+    m.graph_begin([prompt[-1]], [prompt_len])   # eager step at position n, then the captured step
+    engine.sync()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    m.graph_run(steps - 1)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e)
+    m.close()
+    return ms, steps - 1, prefill_s
+
+
 def decode_bs32(engine, spec, steps: int, warmup: int):
     import torch
     from janus_amd import _lib
@@ -217,7 +279,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn"], default="all",
+    ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3"], default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -257,6 +320,21 @@ def main() -> int:
             log(f"  Q4_0 GEMV {n}x{k}: {u2:.2f} us/launch, {a2 / u2 / 1e3:.0f} GB/s")
         copy_gbs = copy_bandwidth()
         log(f"  device copy: {copy_gbs:.0f} GB/s")
+
+    c3 = None
+    if args.only in ("all", "c3") and not args.no_c3:
+        log("config 3: building Llama-2-7B-shape Q4_K model (random init, shared layer bytes)")
+        t0 = time.time()
+        spec2 = llama2_q4k_spec(3, args.layers)
+        log(f"  synthesised in {time.time() - t0:.1f} s")
+        ms3, n3, pre_s = decode_c3(engine, spec2)
+        c3 = {"tok_s": round(n3 / (ms3 / 1e3), 1), "ms_per_token": round(ms3 / n3, 4), "decode_tokens": n3,
+              "prompt": 512, "ctx": 2048, "prefill_s": round(pre_s, 2)}
+        log(f"config 3 Llama-2-7B Q4_K: {ms3 / n3:.3f} ms/token, {c3['tok_s']} tok/s over {n3} decode tokens "
+            f"(context 513-2048)")
+        del spec2
+        if args.only == "c3":
+            return 0
 
     log("building Llama-3-8B-shape Q4_0 model (random init)")
     t0 = time.time()
@@ -301,6 +379,7 @@ def main() -> int:
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
+        "llama2_7b_q4k_c3": c3,
         "attention_c4": attn,
         "cpu_baseline": cpu,
     }

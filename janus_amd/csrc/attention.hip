@@ -281,9 +281,12 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
     }
 }
 
-// Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
+// Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}, in one pass over
+// the splits with a running maximum; the partials of 8 splits are loaded
+// together, so a merge costs ns / 8 dependent round trips.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
+    constexpr int SB = 8;
     const uint32_t h = blockIdx.x, b = blockIdx.y;
     // lengths beyond the planned splits (or the capacity) are clamped, never read past
     const uint32_t span = a.nw * a.chunk;
@@ -291,14 +294,31 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     if (len <= span) return;   // written directly by the partial kernel
     const uint32_t ns = (len + span - 1) / span;
     const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, w[s * (D + 2)]);
-    float L = 0.0f, o = 0.0f;
-    for (uint32_t s = 0; s < ns; ++s) {
-        const float *ws = w + s * (D + 2);
-        float f = fexp2(ws[0] - M);
-        L = fmaf(ws[1], f, L);
-        o = fmaf(ws[2 + threadIdx.x], f, o);
+    float M = -INFINITY, L = 0.0f, o = 0.0f;
+    for (uint32_t s0 = 0; s0 < ns; s0 += SB) {
+        float ms[SB], ls[SB], os[SB];
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const bool in = s0 + j < ns;
+            const float *ws = w + (size_t)(in ? s0 + j : s0) * (D + 2);
+            ms[j] = in ? ws[0] : -INFINITY;
+            ls[j] = in ? ws[1] : 0.0f;
+            os[j] = in ? ws[2 + threadIdx.x] : 0.0f;
+        }
+        float Mn = M;
+#pragma unroll
+        for (int j = 0; j < SB; ++j) Mn = fmaxf(Mn, ms[j]);
+        if (Mn == -INFINITY) continue;   // no live split yet
+        const float r = fexp2(M - Mn);
+        L *= r;
+        o *= r;
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const float f = fexp2(ms[j] - Mn);   // 0 for the padding splits (m = -inf)
+            L = fmaf(ls[j], f, L);
+            o = fmaf(os[j], f, o);
+        }
+        M = Mn;
     }
     put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
 }

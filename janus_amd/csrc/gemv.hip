@@ -284,15 +284,26 @@ struct FQ8_0 {
 struct FQ4_K {
     static constexpr int UNIT = 32;
     static constexpr bool PERM = true;
-    struct W { uint4 q; uint4 hdr; };
+    // The 16-byte super-block header (d, dmin, 12 scale bytes) is shared by
+    // the 8 units of a super-block, which sit on 8 consecutive lanes in every
+    // kernel (units are lane-contiguous and a row holds a multiple of 8): each
+    // lane keeps one header word (lane & 3) and the quad rebuilds the header
+    // with DPP broadcasts at use, 1 VGPR per unit instead of 4.
+    struct W { uint4 q; uint32_t hw; };
     __device__ static W load(WPtr w, size_t unit) {
         size_t sb = unit >> 3;
         int c = (int)(unit & 7);
         const uint4 *blk = (const uint4 *)(w.qs + sb * 144);
         W r;
-        r.hdr = blk[0];
+        r.hw = ((const uint32_t *)blk)[__lane_id() & 3];
         r.q = ld_stream(blk + 1 + c);
         return r;
+    }
+    template <int T> __device__ static uint32_t quad_word(uint32_t v) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, T * 0x55, 0xf, 0xf, false);   // quad_perm [T,T,T,T]
+    }
+    __device__ static uint4 header(const W &w) {
+        return make_uint4(quad_word<0>(w.hw), quad_word<1>(w.hw), quad_word<2>(w.hw), quad_word<3>(w.hw));
     }
     // x for one chunk: 16 low-nibble elements and 16 high-nibble elements.
     struct XF { jf4 lo[4], hi[4]; float slo, shi; int c; };
@@ -373,11 +384,12 @@ struct FQ4_K {
     }
     template <class X>
     __device__ static float finish(const W &w, const X &x, float qlo, float qhi) {
-        float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
+        const uint4 hdr = header(w);
+        float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
         int j = x.c >> 1;
         float sl, ml, sh, mh;
-        scale_min(w.hdr, 2 * j, sl, ml);
-        scale_min(w.hdr, 2 * j + 1, sh, mh);
+        scale_min(hdr, 2 * j, sl, ml);
+        scale_min(hdr, 2 * j + 1, sh, mh);
         float r = (d * sl) * qlo;
         r = fmaf(d * sh, qhi, r);
         r = fmaf(-(dmin * ml), x.slo, r);
