@@ -34,6 +34,11 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes of `bench.py --only roofline`, FETCH_SIZE scaled by 2.0 and
+# WRITE_SIZE by 1.0 (the factors a 1 GiB device copy gives on this device);
+# recorded in profiles/gemv_q4_0_14336x4096_f16.md. Re-measure when the kernel changes.
+ROOFLINE_TRAFFIC_BYTES = 33346621
 METRIC = "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 & 32; GEMV HBM GB/s vs peak"
 L3 = dict(hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256, layers=32, rope_theta=500000.0)
 
@@ -375,7 +380,9 @@ def main() -> int:
                                "F16 LM head, HIP-graph decode step", "layers": args.layers,
                    "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0) per launch, "
+                                       "profiles/gemv_q4_0_14336x4096_f16.md",
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
