@@ -862,21 +862,28 @@ template <bool PERM, int MAXG>
 __device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16 *xs, float *sx16,
                                const float *__restrict__ gamma, float eps, float *red) {
     const uint32_t g16 = (k + 15) / 16;
-    float v[MAXG][16];
+    float v[MAXG][16], gm[MAXG][16];
     float ss = 0.0f;
+    // x and gamma are requested together: one round trip before the reduction
 #pragma unroll
     for (int j = 0; j < MAXG; ++j) {
         const uint32_t g = threadIdx.x + 512u * j, e0 = g * 16;
         if (e0 + 16 <= k) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const jf4 xa = *(const jf4 *)(x + e0 + 4 * q);
+                const jf4 xa = *(const jf4 *)(x + e0 + 4 * q), ga = *(const jf4 *)(gamma + e0 + 4 * q);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) v[j][4 * q + t] = xa[t];
+                for (int t = 0; t < 4; ++t) {
+                    v[j][4 * q + t] = xa[t];
+                    gm[j][4 * q + t] = ga[t];
+                }
             }
         } else {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) v[j][t] = e0 + t < k ? x[e0 + t] : 0.0f;
+            for (int t = 0; t < 16; ++t) {
+                v[j][t] = e0 + t < k ? x[e0 + t] : 0.0f;
+                gm[j][t] = e0 + t < k ? gamma[e0 + t] : 0.0f;
+            }
         }
     }
 #pragma unroll
@@ -891,19 +898,10 @@ __device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16
     const float rms = sqrtf(tot / (float)k + eps);
 #pragma unroll
     for (int j = 0; j < MAXG; ++j) {
-        const uint32_t g = threadIdx.x + 512u * j, e0 = g * 16;
+        const uint32_t g = threadIdx.x + 512u * j;
         if (g >= g16) continue;
-        if (e0 + 16 <= k) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const jf4 ga = *(const jf4 *)(gamma + e0 + 4 * q);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) v[j][4 * q + t] = (v[j][4 * q + t] / rms) * ga[t];
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[j][t] = e0 + t < k ? (v[j][t] / rms) * gamma[e0 + t] : 0.0f;
-        }
+        for (int t = 0; t < 16; ++t) v[j][t] = (v[j][t] / rms) * gm[j][t];
         store_x16<PERM>(v[j], g, xs, sx16);
     }
 }
