@@ -101,6 +101,7 @@ struct GemmArgs {
     uint32_t pitch;        // LDS row pitch of A, in halves
     int c_f16;
     int to_ws;             // write partials to ws even when ksplit == 1 (epilogue kernels read them)
+    uint32_t seg_shift;    // log2 of the 8-half A segments per row of a pass (pass length / 8)
 };
 
 // ---- formats ------------------------------------------------------------------
@@ -248,7 +249,8 @@ struct GF16 {
     }
 };
 
-template <class F> struct Stage { static constexpr int PD = F::CK == 64 ? 4 : 8; };
+// chunks per weight batch (two batches in flight per wavefront)
+template <class F> struct Stage { static constexpr int PD = std::is_same<F, GQ4_0>::value ? 2 : (F::CK == 64 ? 4 : 8); };
 
 // Output element (m, n) of wave-tile value v for lane (32x32 MFMA C layout):
 // n = lane % 32, m = 8 * (v / 4) + 4 * (lane / 32) + v % 4.
@@ -310,29 +312,29 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
         };
         if (active) load(wa, m0);   // in flight while A is staged
 
-        // stage A[0..Mpad)[c0*CK .. c1*CK) as binary16, zero outside rows / k:
-        // every thread issues all of its 16-byte loads before its LDS stores
-        const uint32_t kbase = c0 * F::CK, klen = (c1 - c0) * F::CK;
-        const uint32_t segs_per_row = klen / 8, segs = Mpad * segs_per_row;
+        // stage A[0..Mpad)[c0*CK .. c0*CK + kr) as binary16, zero outside rows / k:
+        // segment s (8 halves) is row s >> seg_shift, column (s & mask) * 8 of the
+        // full pass width (a power of two), so no division; every thread issues
+        // all of its 16-byte loads before its LDS stores
+        const uint32_t kbase = c0 * F::CK;
+        const uint32_t smask = (1u << a.seg_shift) - 1u;
         uint4 sv[SPT];
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const uint32_t s = threadIdx.x + 64u * WAVES * KW * i;
+            const uint32_t m = s >> a.seg_shift, col = kbase + (s & smask) * 8;
             sv[i] = make_uint4(0u, 0u, 0u, 0u);
-            if (s < segs) {
-                const uint32_t m = s / segs_per_row, col = kbase + (s % segs_per_row) * 8;
-                if (m < a.rows && col < a.k) sv[i] = *(const uint4 *)(a.a + (size_t)m * a.k + col);
-            }
+            if (m < a.rows && col < a.k) sv[i] = *(const uint4 *)(a.a + (size_t)m * a.k + col);
         }
         __syncthreads();   // the previous pass is done with LDS
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const uint32_t s = threadIdx.x + 64u * WAVES * KW * i;
-            if (s < segs) *(uint4 *)(As + (size_t)(s / segs_per_row) * a.pitch + (s % segs_per_row) * 8) = sv[i];
+            if ((s >> a.seg_shift) < Mpad) *(uint4 *)(As + (size_t)(s >> a.seg_shift) * a.pitch + (s & smask) * 8) = sv[i];
         }
         if (SUMS) {
             __syncthreads();
-            const uint32_t nsub = klen / 32;
+            const uint32_t nsub = (c1 - c0) * F::CK / 32;
             for (uint32_t i = threadIdx.x; i < nsub * Mpad; i += blockDim.x) {
                 const uint32_t sub = i / Mpad, m = i % Mpad;
                 const _Float16 *p8 = As + (size_t)m * a.pitch + sub * 32;
@@ -567,7 +569,7 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
 
 template <class F, int MT>
 constexpr int gemm_kw() {
-    return (MT == 1 && (std::is_same<F, GQ4_0>::value || std::is_same<F, GF16>::value)) ? 4 : 2;
+    return (MT == 1 && std::is_same<F, GF16>::value) ? 4 : 2;
 }
 
 // kr_force / ks_force (0 = automatic) fix the pass length and the K split.
@@ -577,17 +579,20 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     constexpr int SPT1 = 16 / KW;   // kr = 1024 / MT
     const uint32_t G = (w->n + 31) / 32;
     const uint32_t tiles = (G + WAVES - 1) / WAVES;
-    // K per LDS pass: 1024 (M <= 32) or 512 (M <= 64); narrow products use
-    // half-size passes so that splitting K can still occupy every CU
+    // K per LDS pass: 1024 (M <= 32) or 512 (M <= 64); products with too few
+    // (tile, pass) pairs for two workgroups per CU use half-size passes
+    const uint32_t want = 2u * (uint32_t)ctx->num_cus;
     uint32_t kr = MT == 1 ? 1024 : 512;
-    if (tiles * 4 < (uint32_t)ctx->num_cus && kr / F::CK >= 2 * KW) kr /= 2;
+    if (tiles * ((w->t32_chunks * F::CK + kr - 1) / kr) < want && kr / F::CK >= 2 * KW) kr /= 2;
     if (kr_force) kr = kr_force;
     if (kr % (F::CK * KW) || kr * MT > 2048) return fail(ctx, JANUS_E_INVALID_DIM, "gemm: bad pass length");
     a.pass_chunks = kr / F::CK;
+    a.seg_shift = 0;
+    while ((8u << a.seg_shift) < kr) ++a.seg_shift;
+    if ((8u << a.seg_shift) != kr) return fail(ctx, JANUS_E_INVALID_DIM, "gemm: pass length must be a power of two");
     a.chunks = w->t32_chunks;
     a.total_passes = (a.chunks + a.pass_chunks - 1) / a.pass_chunks;
-    // split K over workgroups only while there are fewer row tiles than CUs
-    const uint32_t want = (uint32_t)ctx->num_cus;
+    // split K over workgroups until there are about two workgroups per CU
     uint32_t ks = (want + tiles - 1) / tiles;
     if (ks_force) ks = ks_force;
     if (ks > a.total_passes) ks = a.total_passes;
