@@ -18,6 +18,8 @@
 //    directly.
 //  * Ragged batches: per-sequence row offsets and lengths are device tables,
 //    so all sequences share one launch.
+#include <type_traits>
+
 #include "internal.h"
 
 namespace janus {
@@ -281,6 +283,247 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
     }
 }
 
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef float af4 __attribute__((ext_vector_type(4)));
+
+// Binary16 caches: one wavefront attends G query heads of one KV head over a
+// position range. The scores of 16 positions x the G heads come from
+// v_mfma_f32_16x16x32_f16 (positions as rows, heads as columns, head dims as
+// K), with q split into binary16 hi + lo parts so the scores keep fp32
+// accuracy (f16 x f16 products are exact; q = hi + lo to 2^-22, after a
+// power-of-two prescale that keeps both parts in range). The softmax runs on
+// the MFMA output layout (lane = head column, 4 positions), publishes P and the
+// rescale factors through a small per-wavefront LDS area, and P.V runs on the
+// VALU in the (position slot, 8-dim slice) layout, so K is read as MFMA
+// operands and V as 128-bit rows. All slots share one running maximum per head,
+// so they merge by plain sums. On return every lane holds (m, l) of head
+// `lane & 15` and the slot-0 lanes hold acc for dims 8 * (lane % (D / 8)).
+template <int D, int G>
+struct MfmaAttn {
+    static constexpr int KS = D / 32;                  // MFMA K steps over the head dims
+    static constexpr int LPP = D / 8, SLOTS = 64 / LPP;
+    static constexpr int BP = 16;                      // positions per MFMA block
+    static constexpr int STEPS = BP / SLOTS;           // P.V steps per block
+    static constexpr int PW = BP * G + G;              // floats of a wavefront's P area
+    static_assert(G <= 16 && (D == 64 || D == 128), "MfmaAttn: G <= 16, D in {64, 128}");
+
+    __device__ static void run(const AttnArgs &a, uint32_t b, uint32_t kvh, uint32_t start, uint32_t end, float *Pw,
+                               float &m, float &l, float (&acc)[G][8]) {
+        const int lane = __lane_id();
+        const int slot = lane / LPP, dl = lane % LPP;   // P.V layout
+        const int col = lane & 15, grp = lane >> 4;     // MFMA layout
+        const uint32_t h0 = kvh * G;
+        const size_t row0 = (size_t)(a.row_base ? (uint32_t)a.row_base[b] : b * a.max_seq);
+        const uint32_t kvrow = a.kv_heads * D;
+        const _Float16 *kc = (const _Float16 *)a.kc + row0 * kvrow + (size_t)kvh * D + 8 * grp;
+        const _Float16 *vc = (const _Float16 *)a.vc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
+
+        uint4 ka[KS], kb[KS], va[STEPS], vb[STEPS];
+        auto load = [&](uint4 (&k)[KS], uint4 (&v)[STEPS], uint32_t p0) {
+            uint32_t kp = p0 + col;
+            kp = kp < end ? kp : end - 1;   // masked below; the address stays inside the sequence
+#pragma unroll
+            for (int t = 0; t < KS; ++t) k[t] = *(const uint4 *)(kc + (size_t)kp * kvrow + 32 * t);
+#pragma unroll
+            for (int u = 0; u < STEPS; ++u) {
+                uint32_t vp = p0 + u * SLOTS + slot;
+                vp = vp < end ? vp : end - 1;
+                v[u] = *(const uint4 *)(vc + (size_t)vp * kvrow);
+            }
+        };
+        // the first batch is requested before q is read and split: its latency
+        // overlaps the q loads
+        if (start < end) load(ka, va, start);
+
+        // q of head `col` (zero for col >= G), dims 8*grp + 32t + i
+        float qv[KS][8];
+        float qmax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+            if (col < G) {
+                const float *qp = a.q + ((size_t)b * a.heads + h0 + col) * D + 8 * grp + 32 * t;
+                const jf4 q0 = *(const jf4 *)qp, q1 = *(const jf4 *)(qp + 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) { qv[t][i] = q0[i]; qv[t][4 + i] = q1[i]; }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) qv[t][i] = 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qmax = fmaxf(qmax, fabsf(qv[t][i]));
+        }
+        qmax = fmaxf(qmax, lane_xor<16>(qmax));
+        qmax = fmaxf(qmax, lane_xor<32>(qmax));
+        int qe = 0;
+        (void)frexpf(qmax, &qe);                  // qmax < 2^qe
+        const int sh = qe > 15 ? qe - 15 : 0;     // |q| * 2^-sh < 2^15
+        const float qs = ldexpf(1.0f, -sh);
+        const float sc2 = a.scale2 * ldexpf(1.0f, sh);
+        ah8 qh[KS], ql[KS];
+#pragma unroll
+        for (int t = 0; t < KS; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = qv[t][i] * qs;
+                const _Float16 hi = (_Float16)x;
+                qh[t][i] = hi;
+                ql[t][i] = (_Float16)(x - (float)hi);
+            }
+
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+        m = -INFINITY;
+        l = 0.0f;
+
+        auto consume = [&](const uint4 (&k)[KS], const uint4 (&v)[STEPS], uint32_t p0) {
+            af4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < KS; ++t) {
+                const ah8 kk = __builtin_bit_cast(ah8, k[t]);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[t], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, ql[t], S, 0, 0, 0);
+            }
+            // S[r]: head col, position p0 + 4*grp + r
+            float sv[4];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool live = p0 + 4 * grp + r < end;
+                sv[r] = live ? S[r] * sc2 : -INFINITY;
+                bm = fmaxf(bm, sv[r]);
+            }
+            bm = fmaxf(bm, lane_xor<16>(bm));
+            bm = fmaxf(bm, lane_xor<32>(bm));
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
+            float ps[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ps[r] = mn == -INFINITY ? 0.0f : fexp2(sv[r] - mn);
+            l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+            m = mn;
+            if (col < G) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Pw[(4 * grp + r) * G + col] = ps[r];
+                if (grp == 0) Pw[BP * G + col] = alpha;
+            }
+            // the area is read by other lanes of this wavefront only: LDS
+            // operations of one wavefront complete in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float al = Pw[BP * G + g];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] *= al;
+            }
+#pragma unroll
+            for (int u = 0; u < STEPS; ++u) {
+                const float *pr = Pw + (u * SLOTS + slot) * G;
+                KVRow<_Float16> vrow;
+                vrow.r = v[u];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float pg = pr[g];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pg, vrow.get(i), acc[g][i]);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        };
+        if (start < end) {
+            uint32_t p0 = start;
+            for (; p0 + BP < end; p0 += 2 * BP) {
+                load(kb, vb, p0 + BP);
+                consume(ka, va, p0);
+                if (p0 + 2 * BP < end) load(ka, va, p0 + 2 * BP);
+                consume(kb, vb, p0 + BP);
+            }
+            if (p0 < end) consume(ka, va, p0);
+        }
+        // slots share the running maximum: sum acc over slots, l over the 4 position groups
+        l += lane_xor<16>(l);
+        l += lane_xor<32>(l);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float x = acc[g][i];
+                if (LPP == 8) x += lane_xor<8>(x);
+                x += lane_xor<16>(x);
+                x += lane_xor<32>(x);
+                acc[g][i] = x;
+            }
+    }
+};
+
+// Work list of (sequence, context piece) x KV head tasks of at most `chunk`
+// positions, enumerated on the device from the length table (ragged batches
+// balance across wavefronts whatever the lengths); a persistent grid of
+// wavefronts walks it. A sequence held by one piece writes its output; the
+// others write (m, l, o) partials for attn_merge_kernel. Requires batch <= 64.
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_task_kernel(AttnArgs a) {
+    using A = MfmaAttn<D, G>;
+    __shared__ float parea[4 * A::PW];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *Pw = parea + wave * A::PW;
+    const uint32_t C = a.chunk;
+    const uint32_t cap = a.splits * C;
+    // lane b: pieces of sequence b (at least one, so an empty sequence writes zeros)
+    uint32_t lenb = 0, nb = 0;
+    if ((uint32_t)lane < a.batch) {
+        lenb = min(min(a.seq_lens ? (uint32_t)a.seq_lens[lane] : a.seq_len, a.max_seq), cap);
+        nb = lenb == 0 ? 1u : (lenb + C - 1) / C;
+    }
+    uint32_t incl = nb;   // inclusive prefix over lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t up = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += up;
+    }
+    const uint32_t pieces = (uint32_t)__shfl((int)incl, 63, 64);
+    const uint32_t ntask = pieces * a.kv_heads;
+    const uint32_t nwave = gridDim.x * 4;
+    for (uint32_t t = blockIdx.x * 4 + wave; t < ntask; t += nwave) {
+        const uint32_t q = t / a.kv_heads, kvh = t % a.kv_heads;
+        // sequence: the number of lanes whose inclusive prefix is <= q
+        const uint64_t le = __ballot(incl <= q);
+        const uint32_t b = (uint32_t)__popcll(le);
+        const uint32_t excl = (uint32_t)__shfl((int)(incl - nb), (int)b, 64);
+        const uint32_t len = (uint32_t)__shfl((int)lenb, (int)b, 64);
+        const uint32_t nseq = (uint32_t)__shfl((int)nb, (int)b, 64);
+        const uint32_t j = q - excl;
+        const uint32_t start = j * C, end = min(len, start + C);
+        float m, l, acc[G][8];
+        A::run(a, b, kvh, start, end, Pw, m, l, acc);
+        // every lane: (m, l) of head lane & 15; slot-0 lanes: acc of dims 8 * dl
+        const int dl = lane % A::LPP;
+        const bool writer = lane < A::LPP;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mg = __shfl(m, g, 64), lg = __shfl(l, g, 64);
+            const uint32_t h = kvh * G + g;
+            if (!writer) continue;
+            if (nseq == 1) {
+                const float inv = 1.0f / fmaxf(lg, 1e-20f);
+                const size_t at = ((size_t)b * a.heads + h) * D + 8 * dl;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) put_out(a, at + i, acc[g][i] * inv);
+            } else {
+                float *w = a.ws + (((size_t)b * a.heads + h) * a.splits + j) * (D + 2);
+                if (dl == 0) { w[0] = mg; w[1] = lg; }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[2 + 8 * dl + i] = acc[g][i];
+            }
+        }
+    }
+}
+
 // Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}, in one pass over
 // the splits with a running maximum; the partials of 8 splits are loaded
 // together, so a merge costs ns / 8 dependent round trips.
@@ -338,6 +581,22 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
     }
     dim3 grid(a.splits, a.kv_heads, a.batch), block(64 * a.nw);
     const size_t lds = (size_t)a.nw * G * (D + 2) * 4;
+    if (std::is_same<KV, _Float16>::value && a.nw == 1) {   // task mode (binary16 caches)
+        const dim3 tgrid(ctx->num_cus * ctx->attn_wpc / 4);
+        switch (G) {
+        case 1: hipLaunchKernelGGL((attn_task_kernel<D, 1>), tgrid, dim3(256), 0, ctx->stream, a); break;
+        case 2: hipLaunchKernelGGL((attn_task_kernel<D, 2>), tgrid, dim3(256), 0, ctx->stream, a); break;
+        case 4: hipLaunchKernelGGL((attn_task_kernel<D, 4>), tgrid, dim3(256), 0, ctx->stream, a); break;
+        case 8: hipLaunchKernelGGL((attn_task_kernel<D, 8>), tgrid, dim3(256), 0, ctx->stream, a); break;
+        default: return fail(ctx, JANUS_E_INVALID_DIM, "attention: heads / kv_heads must be 1, 2, 4 or 8");
+        }
+        JANUS_LAUNCH_CHECK(ctx);
+        if (a.splits > 1) {
+            hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+            JANUS_LAUNCH_CHECK(ctx);
+        }
+        return JANUS_OK;
+    }
     const bool big = a.nw == 16;
     switch (G) {
     case 1:
@@ -371,7 +630,7 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
 // wavefronts merge in LDS, so short contexts need no merge launch; otherwise
 // 4-wavefront workgroups, with a merge kernel across workgroup splits.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out, uint32_t *qh_div_out) {
+                    int kv_f16, uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out, uint32_t *qh_div_out) {
     if (max_len == 0) max_len = 1;
     const uint32_t G = heads / kv_heads;
     // Short contexts with few sequences: one workgroup per query head (the G
@@ -379,9 +638,21 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     // G times more CUs and each wavefront does 1/G of the arithmetic.
     const bool qh = G > 1 && max_len <= 1024 && (uint64_t)batch * heads <= (uint64_t)ctx->num_cus;
     *qh_div_out = qh ? G : 0;
+    const uint64_t waves = (uint64_t)ctx->num_cus * (uint64_t)ctx->attn_wpc;
+    if (kv_f16 && !qh && !ctx->attn_valu && batch >= 2 && batch <= 64) {
+        // task mode for ragged batches (nw = 1): pieces of `chunk` positions,
+        // about two per wavefront when every sequence is max_len long
+        uint64_t c = ctx->attn_task ? ctx->attn_task
+                                    : ((uint64_t)max_len * batch * kv_heads + 2 * waves - 1) / (2 * waves);
+        c = (c + TP - 1) / TP * TP;
+        c = c < 64 ? 64 : (c > 1024 ? 1024 : c);
+        *chunk_out = (uint32_t)c;
+        *nw_out = 1;
+        *splits_out = (uint32_t)((max_len + c - 1) / c);
+        return;
+    }
     const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
-    const uint64_t want = (uint64_t)ctx->num_cus * 8;
-    uint64_t chunk = (max_len * groups + want - 1) / want;
+    uint64_t chunk = (max_len * groups + waves - 1) / waves;
     chunk = (chunk + TP - 1) / TP * TP;
     const uint32_t nw = qh ? 16 : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
     if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
@@ -391,9 +662,9 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
 }
 
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
-                      uint32_t max_len) {
+                      uint32_t max_len, int kv_f16) {
     uint32_t chunk, nw, splits, qh;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits, &qh);
+    attention_plan(ctx, batch, heads, kv_heads, max_len, kv_f16, &chunk, &nw, &splits, &qh);
     if (splits <= 1) return JANUS_OK;
     return ensure_attn_ws(ctx, (size_t)batch * heads * splits * (hd + 2) * sizeof(float));
 }
@@ -418,7 +689,7 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.scale2 = scale * 1.4426950408889634f;
     a.out_f16 = out_f16;
     uint32_t chunk, nw, splits, qh;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, &chunk, &nw, &splits, &qh);
+    attention_plan(ctx, batch, heads, kv_heads, max_len, kv_dt == JANUS_DT_F16, &chunk, &nw, &splits, &qh);
     a.chunk = chunk;
     a.nw = nw;
     a.qh_div = qh;

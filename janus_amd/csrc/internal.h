@@ -23,6 +23,13 @@ struct janus_ctx {
     // binary16 M = 1 products with long rows use the LDS-staged kernel
     // (JANUS_GEMV_KERNEL=reg selects the register-resident one instead).
     bool gemv_lds = true;
+    // binary16-cache attention scores on MFMA (JANUS_ATTN_KERNEL=valu selects
+    // the all-VALU kernel instead, for comparisons).
+    bool attn_valu = false;
+    // attention context split: about this many wavefronts per CU (JANUS_ATTN_WPC)
+    uint32_t attn_wpc = 8;
+    // binary16-cache attention piece length in positions (0: planned; JANUS_ATTN_TASK)
+    uint32_t attn_task = 0;
     // Attention split-K partials; grows on first use and is then reused.
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -149,9 +156,9 @@ int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, voi
                      const int32_t *row_base, const int32_t *positions);
 // Attention split sizing shared by the launch and workspace reservation.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    uint32_t *chunk, uint32_t *nw, uint32_t *splits, uint32_t *qh_div);
+                    int kv_f16, uint32_t *chunk, uint32_t *nw, uint32_t *splits, uint32_t *qh_div);
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
-                      uint32_t max_len);
+                      uint32_t max_len, int kv_f16);
 // out is f32, or binary16 when out_f16 is set.
 int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,

@@ -362,7 +362,8 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
         janus_model_destroy(m);
         return e;
     }
-    if (int e = attention_reserve(ctx, c.max_batch, c.heads, c.kv_heads, c.head_dim, c.max_seq_len)) {
+    if (int e = attention_reserve(ctx, c.max_batch, c.heads, c.kv_heads, c.head_dim, c.max_seq_len,
+                                  c.kv_dtype == JANUS_DT_F16)) {
         janus_model_destroy(m);
         return e;
     }

@@ -236,6 +236,15 @@ int janus_create(int hip_device, janus_ctx **out) {
     }
     ctx->stream = ctx->own_stream;
     if (const char *k = std::getenv("JANUS_GEMV_KERNEL")) ctx->gemv_lds = std::strcmp(k, "reg") != 0;
+    if (const char *k = std::getenv("JANUS_ATTN_KERNEL")) ctx->attn_valu = std::strcmp(k, "valu") == 0;
+    if (const char *k = std::getenv("JANUS_ATTN_WPC")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v >= 1 && v <= 32) ctx->attn_wpc = (uint32_t)v;
+    }
+    if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v >= 16 && v <= 4096) ctx->attn_task = (uint32_t)v;
+    }
     *out = ctx;
     return JANUS_OK;
 }
