@@ -289,9 +289,10 @@ typedef float af4 __attribute__((ext_vector_type(4)));
 // Binary16 caches: one wavefront attends G query heads of one KV head over a
 // position range. The scores of 16 positions x the G heads come from
 // v_mfma_f32_16x16x32_f16 (positions as rows, heads as columns, head dims as
-// K), with q split into binary16 hi + lo parts so the scores keep fp32
-// accuracy (f16 x f16 products are exact; q = hi + lo to 2^-22, after a
-// power-of-two prescale that keeps both parts in range). The softmax runs on
+// K), with q split into binary16 hi + mid + lo parts so the scores keep fp32
+// accuracy (f16 x f16 products are exact; the three parts carry 33
+// significant bits of q, after a power-of-two prescale that keeps them in
+// range). The softmax runs on
 // the MFMA output layout (lane = head column, 4 positions), publishes P and the
 // rescale factors through a small per-wavefront LDS area, and P.V runs on the
 // VALU in the (position slot, 8-dim slice) layout, so K is read as MFMA
@@ -359,15 +360,18 @@ struct MfmaAttn {
         const int sh = qe > 15 ? qe - 15 : 0;     // |q| * 2^-sh < 2^15
         const float qs = ldexpf(1.0f, -sh);
         const float sc2 = a.scale2 * ldexpf(1.0f, sh);
-        ah8 qh[KS], ql[KS];
+        ah8 qh[KS], qm[KS], ql[KS];   // x = hi + mid + lo: 33 significant bits, more than fp32's 24
 #pragma unroll
         for (int t = 0; t < KS; ++t)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float x = qv[t][i] * qs;
                 const _Float16 hi = (_Float16)x;
+                const float r = x - (float)hi;
+                const _Float16 mid = (_Float16)r;
                 qh[t][i] = hi;
-                ql[t][i] = (_Float16)(x - (float)hi);
+                qm[t][i] = mid;
+                ql[t][i] = (_Float16)(r - (float)mid);
             }
 
 #pragma unroll
@@ -382,8 +386,9 @@ struct MfmaAttn {
 #pragma unroll
             for (int t = 0; t < KS; ++t) {
                 const ah8 kk = __builtin_bit_cast(ah8, k[t]);
-                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[t], S, 0, 0, 0);
                 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, ql[t], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qm[t], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[t], S, 0, 0, 0);
             }
             // S[r]: head col, position p0 + 4*grp + r
             float sv[4];
