@@ -857,7 +857,7 @@ __device__ __forceinline__ void store_x16(const float (&v)[16], uint32_t g, _Flo
 // RMS-normalised staging of f32 x (512-thread workgroups, k <= 16 * 512 * MAXG):
 // every thread loads its 16-element groups once, with all loads in flight
 // together; the sum of squares is reduced over the workgroup in a fixed order
-// (thread order, then wavefront order), then x / rms * gamma is staged.
+// (thread order, then wavefront order), then x * (1 / rms) * gamma is staged.
 template <bool PERM, int MAXG>
 __device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16 *xs, float *sx16,
                                const float *__restrict__ gamma, float eps, float *red) {
@@ -895,13 +895,15 @@ __device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16
     __syncthreads();
     float tot = 0.0f;
     for (uint32_t w = 0; w < (blockDim.x >> 6); ++w) tot += red[w];
-    const float rms = sqrtf(tot / (float)k + eps);
+    // x * (1 / rms) instead of x / rms: within one ulp, and the staged value
+    // is rounded to binary16 right after
+    const float inv = 1.0f / sqrtf(tot / (float)k + eps);
 #pragma unroll
     for (int j = 0; j < MAXG; ++j) {
         const uint32_t g = threadIdx.x + 512u * j;
         if (g >= g16) continue;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v[j][t] = (v[j][t] / rms) * gm[j][t];
+        for (int t = 0; t < 16; ++t) v[j][t] = (v[j][t] * inv) * gm[j][t];
         store_x16<PERM>(v[j], g, xs, sx16);
     }
 }
