@@ -102,6 +102,7 @@ struct GemmArgs {
     int c_f16;
     int to_ws;             // write partials to ws even when ksplit == 1 (epilogue kernels read them)
     uint32_t seg_shift;    // log2 of the 8-half A segments per row of a pass (pass length / 8)
+    int swiglu;            // ksplit == 1 only: rows (2j, 2j+1) are (gate_j, up_j); c = silu(gate)*up, binary16 [rows][n/2]
 };
 
 // ---- formats ------------------------------------------------------------------
@@ -277,6 +278,27 @@ __device__ __forceinline__ void store_tile(const GemmArgs &a, uint32_t g, int la
         }
 }
 
+// SwiGLU store of a finished tile: columns 2j, 2j+1 (lanes l, l^1) hold gate_j
+// and up_j of the same rows; the even lane writes silu(gate) * up as binary16
+// (the arithmetic of elementwise_kernel's SwiGLU).
+template <int MT>
+__device__ __forceinline__ void store_swiglu(const GemmArgs &a, uint32_t g, int lane, const f16x (&acc)[MT]) {
+    const uint32_t n = g * 32 + (lane & 31);
+    const uint32_t half = a.n / 2;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float mine = acc[mt][v];
+            const float other = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mine), 0xb1, 0xf, 0xf, false));
+            const uint32_t m = out_row(mt, v, lane);
+            if (!(lane & 1) && m < a.rows && n + 1 < a.n) {
+                const float act = mine * (1.0f / (1.0f + expf(-mine))) * other;
+                ((uint16_t *)a.c)[(size_t)m * half + n / 2] = f2h_bits(act);
+            }
+        }
+}
+
 // KW wavefronts per row group, each on a K slice of the pass (4 where the
 // format's registers fit 4 wavefronts per SIMD, else 2).
 // SPT: 16-byte A segments per thread per pass, Mpad * kr / 8 / (256 * KW).
@@ -383,7 +405,8 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
     }
     if (kw != 0 || !active) return;
     if (a.ksplit == 1 && !a.to_ws) {
-        store_tile<MT>(a, g, lane, acc);
+        if (a.swiglu) store_swiglu<MT>(a, g, lane, acc);
+        else store_tile<MT>(a, g, lane, acc);
         return;
     }
     // split-K: this split's tile goes to the workspace; gemm_reduce_kernel adds
@@ -830,6 +853,15 @@ int gemm_qkv_rope(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32
 
 int gemm_swiglu(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, void *act16) {
     if (w->n % 2) return fail(ctx, JANUS_E_INVALID_DIM, "swiglu epilogue: odd row count");
+    const uint32_t tiles = (w->n + 32 * WAVES - 1) / (32 * WAVES);
+    if (w->type == JANUS_DT_Q4_0 && rows <= 32 && 4 * tiles >= 3 * (uint32_t)ctx->num_cus) {
+        // enough row tiles for every CU without splitting K: 16-wavefront
+        // workgroups over the whole K, SwiGLU applied to the finished tile
+        if (int e = mfma_gemm_prepare(ctx, w)) return e;
+        GemmArgs g = make_args(w, a16, act16, 1, rows, nullptr);
+        g.swiglu = 1;
+        return launch_mfma<GQ4_0, 1, 4, 2>(ctx, g, w, nullptr, 1024, 1);
+    }
     GemmPartials p{};
     if (int r = run_partials(ctx, a16, w, rows, &p)) return r;
     const size_t total = (size_t)rows * (w->n / 2);

@@ -117,10 +117,10 @@ def test_ragged_batch_equals_single_sequences(engine, spec):
     mb.close()
 
 
-def _mini_llama3(seed=11, qtype=synth.Q4_0):
+def _mini_llama3(seed=11, qtype=synth.Q4_0, ffn=1024):
     """A 2-layer Llama-3-shaped model (head_dim 128, GQA 4:1, theta 5e5) small
     enough for the oracle: exercises the fused single-sequence path."""
-    return synth.make_model(seed, 512, 4, 1, 1024, 1000, 2, qtype, 1e-5, 500000.0,
+    return synth.make_model(seed, 512, 4, 1, ffn, 1000, 2, qtype, 1e-5, 500000.0,
                             embed_type=synth.F16, head_type=synth.F16)
 
 
@@ -173,14 +173,16 @@ def test_fused_graph_matches_fused_eager(engine):
     assert outs[0] == outs[1]
 
 
-@pytest.mark.parametrize("qtype,kv_dtype", [(synth.Q4_0, _lib.DT_F16), (synth.Q4_K, _lib.DT_F16),
-                                             (synth.Q8_0, _lib.DT_F32)])
-def test_batched_f16_path_equals_single_sequences(engine, qtype, kv_dtype):
+@pytest.mark.parametrize("qtype,kv_dtype,ffn", [(synth.Q4_0, _lib.DT_F16, 1024), (synth.Q4_K, _lib.DT_F16, 1024),
+                                                 (synth.Q8_0, _lib.DT_F32, 1024), (synth.Q4_0, _lib.DT_F16, 12288)])
+def test_batched_f16_path_equals_single_sequences(engine, qtype, kv_dtype, ffn):
     """Ragged batch with binary16 activations (fused batched step: MFMA
     products with RoPE/KV-append, residual+RMSNorm and SwiGLU epilogues,
     per-sequence positions) against each sequence run alone on the fused
-    single-sequence GEMV path, and against the oracle."""
-    spec = _mini_llama3(17, qtype)
+    single-sequence GEMV path, and against the oracle. FFN 12288 gives the
+    gate/up product enough row tiles to run unsplit with SwiGLU applied in
+    the product's own store."""
+    spec = _mini_llama3(17, qtype, ffn)
     rng = np.random.default_rng(19)
     lens = [5, 12, 8]
     prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
