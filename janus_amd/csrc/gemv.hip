@@ -519,14 +519,6 @@ __device__ __forceinline__ float reduce_rows(float (&v)[R], int li, int &ridx) {
 
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_QKV_ROPE = 2, EPI_SWIGLU = 3, EPI_ARGMAX = 4 };
 
-// Order-preserving key of a float (larger value -> larger key); NaN maps to 0
-// so it never wins. Packed with the row index below it, the maximum key is
-// the largest value and, among equal values, the last index.
-__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
-    const uint32_t u = __float_as_uint(v);
-    const uint32_t k = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
-    return ((uint64_t)k << 32) | idx;
-}
 
 struct GemvArgs {
     WPtr w;

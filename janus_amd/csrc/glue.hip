@@ -279,6 +279,59 @@ int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vo
     return JANUS_OK;
 }
 
+// Each workgroup scans 8192 logits of one row (8 float4 per thread, all loads
+// in flight together) and each wavefront posts one atomicMax of its best key.
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restrict__ logits,
+                                                          unsigned long long *best, uint32_t vocab) {
+    const uint32_t row = blockIdx.y;
+    const float *l = logits + (size_t)row * vocab;
+    const uint32_t base = blockIdx.x * 8192u + threadIdx.x * 4u;
+    uint64_t key = 0;
+    float4 v[8];
+    const bool vec = (vocab & 3u) == 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t i = base + 1024u * j;
+        if (vec && i + 4 <= vocab) {
+            v[j] = *(const float4 *)(l + i);
+        } else {
+            v[j].x = i < vocab ? l[i] : -INFINITY;
+            v[j].y = i + 1 < vocab ? l[i + 1] : -INFINITY;
+            v[j].z = i + 2 < vocab ? l[i + 2] : -INFINITY;
+            v[j].w = i + 3 < vocab ? l[i + 3] : -INFINITY;
+        }
+    }
+    auto take = [&](float x, uint32_t i) {
+        if (i < vocab) {
+            const uint64_t k = argmax_key(x, i);
+            key = k > key ? k : key;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t i = base + 1024u * j;
+        take(v[j].x, i);
+        take(v[j].y, i + 1);
+        take(v[j].z, i + 2);
+        take(v[j].w, i + 3);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t other = ((uint64_t)(uint32_t)shfl_xor((int)(key >> 32), o) << 32) |
+                               (uint32_t)shfl_xor((int)(key & 0xffffffffu), o);
+        key = other > key ? other : key;
+    }
+    if ((threadIdx.x & 63) == 0 && key) atomicMax(best + row, (unsigned long long)key);
+}
+
+int argmax_keys_launch(janus_ctx *ctx, const float *logits, unsigned long long *best, uint32_t vocab,
+                       uint32_t batch) {
+    hipLaunchKernelGGL(argmax_keys_kernel, dim3((vocab + 8191) / 8192, batch), dim3(256), 0, ctx->stream, logits, best,
+                       vocab);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
 // Sequential in context order so repeated ids compound exactly as the host loop.
 __global__ void penalty_kernel(float *logits, uint32_t vocab, const int32_t *__restrict__ ctx_ids, uint32_t n,
                                float penalty) {

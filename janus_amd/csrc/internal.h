@@ -167,6 +167,11 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
 int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
                  uint32_t batch, float *out);
 int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie);
+// Last-max argmax of each row as a running atomicMax of argmax_key into
+// best[row] (zero before the call; the caller reads and clears it), the
+// rows split over many workgroups.
+int argmax_keys_launch(janus_ctx *ctx, const float *logits, unsigned long long *best, uint32_t vocab,
+                       uint32_t batch);
 int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t *ids, uint32_t n, float penalty);
 
 }  // namespace janus
@@ -218,6 +223,15 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) {
 
 template <typename T> __device__ __forceinline__ T shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, 64);
+}
+
+// Order-preserving key of a float (larger value -> larger key); NaN maps to 0
+// so it never wins. Packed with the index below it, the maximum key is the
+// largest value and, among equal values, the last index (argmax "last max").
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t k = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    return ((uint64_t)k << 32) | idx;
 }
 
 // Sum over all 64 lanes of a wavefront; every lane receives the total.

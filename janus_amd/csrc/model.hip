@@ -606,12 +606,16 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
         ctx->stream = user;
         return hip_fail(ctx, be, "hipStreamBeginCapture");
     }
+    // the greedy token: folded into the single-sequence LM head, a keyed
+    // atomicMax over the logits of a batch, or the plain argmax kernel
     const bool fold = use_fused1(m, nseq) && can_fold_argmax(m);
+    const bool keys = !fold && nseq > 1;
     e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, fold);
-    if (!e && !fold) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
+    if (!e && keys) e = argmax_keys_launch(ctx, m->logits, m->d_best, m->cfg.vocab, nseq);
+    else if (!e && !fold) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
     if (!e) {
         hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq,
-                           fold ? m->d_best : nullptr, m->d_tokens);
+                           (fold || keys) ? m->d_best : nullptr, m->d_tokens);
         if (hipGetLastError() != hipSuccess) e = JANUS_E_HIP;
     }
     hipGraph_t g = nullptr;
