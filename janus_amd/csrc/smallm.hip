@@ -428,7 +428,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, uint32_t M
     const float *p = a.ws + (size_t)m * Npad + n;
     const size_t stride = (size_t)Mpad * Npad;
     float s = 0.0f;
-    for (uint32_t j = 0; j < a.ksplit; ++j) s += __builtin_nontemporal_load(p + j * stride);
+    for (uint32_t j = 0; j < a.ksplit; ++j) s += p[j * stride];
     if (a.resid) s += a.resid[idx];
     if (a.c_f16) ((uint16_t *)a.c)[idx] = f2h_bits(s);
     else ((float *)a.c)[idx] = s;
@@ -697,7 +697,7 @@ __device__ __forceinline__ V sum_splits(const float *q, size_t stride, uint32_t 
         V u[8];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
-            if (k0 + kk < ksplit) u[kk] = __builtin_nontemporal_load((const V *)(q + (k0 + kk) * stride));
+            if (k0 + kk < ksplit) u[kk] = *(const V *)(q + (k0 + kk) * stride);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
             if (k0 + kk < ksplit) s += u[kk];
