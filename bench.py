@@ -14,6 +14,11 @@ Workload (BASELINE.json metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
     (config 2: x fp16, fp32 accumulate, fp16 output), timed with HIP events over
     graph-replayed back-to-back launches rotating through > 256 MB of weight
     copies so the Infinity Cache cannot serve them.
+  * gemm_m32_q4_0: the config-5 small-M product at the four layer shapes
+    (32 binary16 rows, MFMA GEMM + split-K reduce), GB/s and the fraction of
+    dense fp16 MFMA peak.
+  * llama2_7b_q4k_c3: config 3 (Llama-2-7B shape, Q4_K, decode to 2048 ctx).
+  * attention_c4: config 4 (16 ragged sequences, GQA 32/8, fp16 KV).
   * cpu_baseline: the CPU oracle (a restatement of the reference arithmetic, not
     the reference itself) on the same model, one thread, a bounded sample.
 
@@ -34,6 +39,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0    # dense fp16 MFMA, MI355X
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of `bench.py --only roofline`, FETCH_SIZE scaled by 2.0 and
 # WRITE_SIZE by 1.0 (the factors a 1 GiB device copy gives on this device);
@@ -205,6 +211,44 @@ def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
     return us, algo, copies
 
 
+def gemm_m32(engine, n: int, k: int, rows: int = 32, launches: int = 100):
+    """The small-M product of config 5 at one layer shape: 32 binary16 rows x a
+    Q4_0 weight (MFMA GEMM + split-K reduce, fp16 output) through
+    janus_gemm_auto, graph-replayed over > 400 MB of weight copies. Returns
+    (us per launch, algorithmic bytes, flops)."""
+    import torch
+    from janus_amd import ops, synth
+    rng = np.random.default_rng(12)
+    raw = synth.random_q4_0(rng, n, k)
+    copies = max(2, int(np.ceil(400e6 / raw.nbytes)))
+    ws = [ops.GpuTensor(engine, ops.DT_Q4_0, n, k, raw) for _ in range(copies)]
+    a = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float16)).cuda()
+    y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
+    for i in range(copies):
+        ops.gemm_auto(engine, a, ws[i], y, rows, 1, k, n)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        engine.bind_stream(side)
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(launches):
+                ops.gemm_auto(engine, a, ws[i % copies], y, rows, 1, k, n)
+    engine.bind_stream()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = 1e30
+    for _ in range(5):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        graph.replay()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e))
+    del graph, ws
+    return best * 1e3 / launches, raw.nbytes + 2 * rows * k + 2 * rows * n, 2.0 * rows * n * k
+
+
 def attention_c4(engine, reps: int = 20):
     """16 ragged sequences, ctx ~ U[128, 8192], 32 query / 8 KV
     heads, head_dim 128, fp16 Q/K/V ~ N(0, 1), scale 1/sqrt(128), fp32 softmax,
@@ -285,7 +329,7 @@ def main() -> int:
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3"], default="all",
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3", "gemm"], default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -309,6 +353,17 @@ def main() -> int:
                 "algorithmic_bytes": a_bytes}
         log(f"attention C4: {a_us:.1f} us/launch, {a_bytes / a_us / 1e3:.0f} GB/s (ctx sum {a_rows})")
         if args.only == "attn":
+            return 0
+    gemm = None
+    if args.only in ("all", "gemm"):
+        gemm = {}
+        for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)):
+            u, b, fl = gemm_m32(engine, n, k)
+            gemm[f"{n}x{k}"] = {"us_per_launch": round(u, 2), "GB_s": round(b / u / 1e3, 1),
+                                "TFLOP_s": round(fl / u / 1e6, 1), "mfma_frac": round(fl / u / 1e6 / MFMA_PEAK_TFLOPS, 4)}
+            log(f"  Q4_0 GEMM M=32 {n}x{k}: {u:.2f} us, {b / u / 1e3:.0f} GB/s, {fl / u / 1e6:.0f} TFLOP/s "
+                f"({fl / u / 1e6 / MFMA_PEAK_TFLOPS:.3f} of dense fp16 MFMA)")
+        if args.only == "gemm":
             return 0
     if args.only in ("all", "roofline"):
         log("roofline: Q4_0 GEMV 14336x4096")
@@ -386,6 +441,7 @@ def main() -> int:
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
+        "gemm_m32_q4_0": gemm,
         "llama2_7b_q4k_c3": c3,
         "attention_c4": attn,
         "cpu_baseline": cpu,

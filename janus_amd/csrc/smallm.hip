@@ -427,8 +427,16 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, uint32_t M
     const uint32_t m = (uint32_t)(idx / a.n), n = (uint32_t)(idx % a.n);
     const float *p = a.ws + (size_t)m * Npad + n;
     const size_t stride = (size_t)Mpad * Npad;
+    // split order; the loads of 8 splits are issued together
     float s = 0.0f;
-    for (uint32_t j = 0; j < a.ksplit; ++j) s += p[j * stride];
+    for (uint32_t j0 = 0; j0 < a.ksplit; j0 += 8) {
+        float u[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) u[jj] = j0 + jj < a.ksplit ? p[(j0 + jj) * stride] : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            if (j0 + jj < a.ksplit) s += u[jj];
+    }
     if (a.resid) s += a.resid[idx];
     if (a.c_f16) ((uint16_t *)a.c)[idx] = f2h_bits(s);
     else ((float *)a.c)[idx] = s;
