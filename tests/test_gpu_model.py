@@ -236,3 +236,24 @@ def test_batched_graph_matches_batched_eager(engine):
         outs.append([list(map(int, t)) for t in toks])
         m.close()
     assert outs[0] == outs[1]
+
+
+def test_batched_40_sequences_two_m_tiles(engine):
+    """40 sequences: the fused batched step runs its products with two 32-row
+    MFMA tiles; every sequence must match its own single-sequence run."""
+    spec = _mini_llama3(31)
+    rng = np.random.default_rng(37)
+    B = 40
+    lens = rng.integers(1, 9, B).tolist()
+    prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
+    mb = Model(engine, spec, max_seq_len=16, max_batch=B, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    for step in range(max(lens)):
+        mb.forward([pr[min(step, len(pr) - 1)] for pr in prompts], [min(step, len(pr) - 1) for pr in prompts])
+    out = mb.logits(B)
+    mb.close()
+    for s in (0, 17, 31, 32, 39):
+        m = Model(engine, spec, max_seq_len=16, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for p, t in enumerate(prompts[s]):
+            m.forward([t], [p])
+        assert _rel_err(out[s], m.logits()[0]) <= 1e-3, s
+        m.close()
