@@ -44,7 +44,7 @@ MFMA_PEAK_TFLOPS = 2500.0    # dense fp16 MFMA, MI355X
 # WRITE_SIZE passes of `bench.py --only roofline`, FETCH_SIZE scaled by 2.0 and
 # WRITE_SIZE by 1.0 (the factors a 1 GiB device copy gives on this device);
 # recorded in profiles/gemv_q4_0_14336x4096_f16.md. Re-measure when the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 33346621
+ROOFLINE_TRAFFIC_BYTES = 33366077
 METRIC = "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 & 32; GEMV HBM GB/s vs peak"
 L3 = dict(hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256, layers=32, rope_theta=500000.0)
 
