@@ -1,6 +1,6 @@
 """Decode benchmark: Llama-3-8B-shape Q4_0 greedy decode on one MI355X.
 
-Workload (BASELINE.json metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
+Workload (headline metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
 32; GEMV HBM GB/s vs peak"):
   * value: batch-1 greedy decode tok/s of a random-init Llama-3-8B-architecture
     model (32 layers, hidden 4096, 32/8 heads, FFN 14336, vocab 128256, RoPE
@@ -8,7 +8,7 @@ Workload (BASELINE.json metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
     fp16 activations into the products. A 128-token prompt is prefilled, then
     each timed step is one HIP-graph decode step (embed -> 32 layers -> LM head
     -> argmax fed back as the next token).
-  * bs32: the ragged continuous-batch step of BASELINE config 5 (32 sequences,
+  * bs32: the ragged continuous-batch step of benchmark configuration 5 (32 sequences,
     fp16 KV contexts uniform in [256, 4096], one forward pass per step).
   * roofline: the dominant kernel, the Q4_0 GEMV at the 14336x4096 decode shape
     (config 2: x fp16, fp32 accumulate, fp16 output), timed with HIP events over
@@ -87,7 +87,7 @@ L2 = dict(hidden=4096, heads=32, kv_heads=32, ffn=11008, vocab=32000, layers=32,
 
 
 def llama2_q4k_spec(seed: int, layers: int = 32):
-    """BASELINE config 3 architecture (Llama-2-7B: 32 layers, hidden 4096, 32 MHA
+    """benchmark configuration 3 architecture (Llama-2-7B: 32 layers, hidden 4096, 32 MHA
     heads, FFN 11008, vocab 32000) with Q4_K blocks quantised from N(0, 0.02).
     Quantising 6.7 B weights in numpy takes minutes, so one 4096x4096, one
     11008x4096 and one 4096x11008 matrix are quantised and their bytes reused
@@ -119,7 +119,7 @@ def llama2_q4k_spec(seed: int, layers: int = 32):
 
 
 def decode_c3(engine, spec, prompt_len: int = 512, ctx: int = 2048):
-    """BASELINE config 3 workload: a 512-token random-id prompt prefilled token
+    """benchmark configuration 3 workload: a 512-token random-id prompt prefilled token
     by token, then greedy decode to a 2048-token context (HIP-graph steps), fp16
     KV, batch 1. Returns (decode ms total, decode tokens, prefill s)."""
     import torch
@@ -250,7 +250,7 @@ def gemm_m32(engine, n: int, k: int, rows: int = 32, launches: int = 100):
 
 
 def attention_c4(engine, reps: int = 20):
-    """16 ragged sequences, ctx ~ U[128, 8192], 32 query / 8 KV
+    """benchmark configuration 4: 16 ragged sequences, ctx ~ U[128, 8192], 32 query / 8 KV
     heads, head_dim 128, fp16 Q/K/V ~ N(0, 1), scale 1/sqrt(128), fp32 softmax,
     packed into one launch through a prefix-sum row-offset table. Returns
     (us per launch, algorithmic bytes, total context)."""

@@ -30,6 +30,9 @@ struct janus_ctx {
     uint32_t attn_wpc = 8;
     // binary16-cache attention piece length in positions (0: planned; JANUS_ATTN_TASK)
     uint32_t attn_task = 0;
+    // small-M quantised GEMMs over several K passes per workgroup use the
+    // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
+    bool gemm_pipe = true;
     // Attention split-K partials; grows on first use and is then reused.
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;

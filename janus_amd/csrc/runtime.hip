@@ -241,6 +241,7 @@ int janus_create(int hip_device, janus_ctx **out) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 1 && v <= 32) ctx->attn_wpc = (uint32_t)v;
     }
+    if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 16 && v <= 4096) ctx->attn_task = (uint32_t)v;

@@ -420,6 +420,178 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
 }
 
 // Sums the split-K partials in split order and applies the epilogue.
+// Cross-pass pipelined form of gemm_mfma_kernel for the quantised formats,
+// with the pass length KR fixed at compile time. A is double-buffered in LDS:
+// the activations of pass p + 1 are requested while pass p computes and are
+// stored at its end; each wavefront keeps one pass of weight chunks in
+// registers and requests chunk i of the next pass as soon as chunk i of the
+// current one is consumed, so a pass's weights are in flight during the
+// previous pass and the barrier between them. One barrier per pass (two for
+// Q4_K, whose activation sums are built from the staged pass). Products,
+// scale rounding, slice order and outputs are those of gemm_mfma_kernel.
+template <class F, int MT, int KW, int KR>
+__global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
+    constexpr int NT = 64 * WAVES * KW;   // threads
+    constexpr int PC = KR / F::CK;        // chunks per pass
+    constexpr int CPW = PC / KW;          // chunks per wavefront per pass
+    constexpr int MP = MT * 32;           // padded rows
+    constexpr int PITCH = KR + 8;         // LDS row pitch in halves
+    constexpr int SEGS = KR / 8;          // 16-byte segments per row of a pass
+    constexpr int SPT = MP * SEGS / NT;   // segments per thread
+    static_assert(CPW >= 1 && CPW * KW == PC && SPT >= 1 && SPT * NT == MP * SEGS, "pass shape");
+    constexpr uint32_t ABYTES = (uint32_t)MP * PITCH * 2;
+    constexpr uint32_t BUF = (ABYTES + (SUMS ? (uint32_t)(KR / 32) * MP * 4 : 0u) + 15u) / 16u * 16u;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rgw = wave % WAVES, kw = wave / WAVES;
+    const uint32_t G = (a.n + 31) / 32;
+    const uint32_t g = blockIdx.x * WAVES + rgw, ks = blockIdx.y;
+    const bool active = g < G;
+    const uint32_t p_begin = ks * a.passes_per_wg;
+    const uint32_t p_end = min(a.total_passes, p_begin + a.passes_per_wg);
+
+    f16x acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = (f16x){};
+    typename F::W w[CPW];
+    uint4 sv[SPT];
+
+    // Every wavefront issues the same sequence of loads whatever the shape
+    // (addresses clamped into range, out-of-range A zeroed when stored,
+    // inactive wavefronts stream a real row group and discard it), so the
+    // compiler's load counters stay exact and no wait covers a later load.
+    const uint32_t gl = active ? g : G - 1;
+    auto load_a = [&](uint32_t p) {
+        const uint32_t kbase = p * KR;
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const uint32_t s = threadIdx.x + NT * i;
+            const uint32_t m = min(s / SEGS, a.rows - 1), col = min(kbase + (s % SEGS) * 8, a.k - 8);
+            sv[i] = *(const uint4 *)(a.a + (size_t)m * a.k + col);
+        }
+    };
+    auto store_a = [&](uint32_t p) {
+        _Float16 *As = (_Float16 *)(smem + (p & 1) * BUF);
+        const uint32_t kbase = p * KR;
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const uint32_t s = threadIdx.x + NT * i;
+            const bool ok = s / SEGS < a.rows && kbase + (s % SEGS) * 8 < a.k;
+            *(uint4 *)(As + (s / SEGS) * PITCH + (s % SEGS) * 8) = ok ? sv[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    // Q4_K: per-(sub-block, row) sums of the staged activations, as gemm_mfma_kernel
+    auto sums = [&](uint32_t p) {
+        const _Float16 *As = (const _Float16 *)(smem + (p & 1) * BUF);
+        float *Ss = (float *)(smem + (p & 1) * BUF + ABYTES);
+        const uint32_t c0 = p * PC, c1 = min(a.chunks, c0 + PC);
+        const uint32_t n = (c1 - c0) * F::CK / 32 * MP;
+        for (uint32_t i = threadIdx.x; i < n; i += NT) {
+            const _Float16 *p8 = As + (i % MP) * PITCH + (i / MP) * 32;
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) t += (float)p8[j];
+            Ss[i] = t;
+        }
+    };
+    // chunk i of this wavefront's slice of pass p (K-tail slots repeat the
+    // pass's last chunk and are not computed)
+    auto chunk_of = [&](uint32_t p, int i) {
+        return min(p * PC + kw * CPW + i, min(a.chunks, (p + 1) * PC) - 1);
+    };
+    // compute pass p from LDS buffer p & 1; with LOAD, request chunk i of pass
+    // p + 1 into slot i as soon as slot i is consumed
+    auto pass = [&](uint32_t p, auto load_next) {
+        const _Float16 *As = (const _Float16 *)(smem + (p & 1) * BUF);
+        const float *Ss = (const float *)(smem + (p & 1) * BUF + ABYTES);
+        const uint32_t c1 = min(a.chunks, (p + 1) * PC), m0 = p * PC + kw * CPW;
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+            if (m0 + i < c1) F::template mma<MT>(w[i], As, PITCH, (uint32_t)(kw * CPW + i) * F::CK, lane, Ss, 0, acc);
+            if (decltype(load_next)::value) w[i] = F::load(a, gl, chunk_of(p + 1, i), lane);
+        }
+    };
+
+    if (p_begin < p_end) {
+        const uint32_t last = p_end - 1;
+        load_a(p_begin);
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) w[i] = F::load(a, gl, chunk_of(p_begin, i), lane);
+        store_a(p_begin);
+        load_a(min(p_begin + 1, last));
+        __syncthreads();
+        if (SUMS) {
+            sums(p_begin);
+            __syncthreads();
+        }
+        for (uint32_t p = p_begin; p < last; ++p) {
+            pass(p, std::true_type{});
+            store_a(p + 1);   // that buffer was last read in pass p - 1
+            load_a(min(p + 2, last));
+            __syncthreads();
+            if (SUMS) {
+                sums(p + 1);
+                __syncthreads();
+            }
+        }
+        pass(last, std::false_type{});
+    }
+
+    if (KW > 1) {
+        float *red = (float *)smem;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[((size_t)wave * 16 + v) * 64 + lane] = acc[mt][v];
+            __syncthreads();
+            if (kw == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float sum = red[((size_t)rgw * 16 + v) * 64 + lane];
+                    for (int j = 1; j < KW; ++j) sum += red[((size_t)(j * WAVES + rgw) * 16 + v) * 64 + lane];
+                    acc[mt][v] = sum;
+                }
+            }
+        }
+    }
+    if (kw != 0 || !active) return;
+    if (a.ksplit == 1 && !a.to_ws) {
+        if (a.swiglu) store_swiglu<MT>(a, g, lane, acc);
+        else store_tile<MT>(a, g, lane, acc);
+        return;
+    }
+    const uint32_t Npad = G * 32, n = g * 32 + (lane & 31);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            __builtin_nontemporal_store(acc[mt][v], a.ws + ((size_t)ks * MP + out_row(mt, v, lane)) * Npad + n);
+}
+
+// LDS bytes of gemm_pipe_kernel: two A buffers (with Q4_K sums), at least the
+// K-slice reduction area.
+template <class F, int MT, int KW, int KR>
+constexpr size_t pipe_lds() {
+    constexpr size_t abytes = (size_t)MT * 32 * (KR + 8) * 2;
+    constexpr size_t buf = (abytes + (std::is_same<F, GQ4_K>::value ? (size_t)(KR / 32) * MT * 32 * 4 : 0) + 15) / 16 * 16;
+    constexpr size_t red = (size_t)WAVES * KW * 16 * 64 * 4;
+    return 2 * buf > red ? 2 * buf : red;
+}
+
+template <class F, int MT, int KW, int KR>
+void launch_pipe(janus_ctx *ctx, dim3 grid, const GemmArgs &a) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void *)gemm_pipe_kernel<F, MT, KW, KR>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    constexpr size_t lds = pipe_lds<F, MT, KW, KR>();
+    hipLaunchKernelGGL((gemm_pipe_kernel<F, MT, KW, KR>), grid, dim3(64 * WAVES * KW), lds, ctx->stream, a);
+}
+
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, uint32_t Mpad) {
     const uint32_t Npad = (a.n + 31) / 32 * 32;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -615,6 +787,26 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     const uint32_t want = 2u * (uint32_t)ctx->num_cus;
     uint32_t kr = MT == 1 ? 1024 : 512;
     if (tiles * ((w->t32_chunks * F::CK + kr - 1) / kr) < want && kr / F::CK >= 2 * KW) kr /= 2;
+    uint32_t ks = 0;
+    bool pipe = false;
+    if constexpr (!std::is_same<F, GF16>::value) {
+        // pipelined kernel (quantised weights): 256-long passes, K split until
+        // about 1.1 workgroups per CU, used when every workgroup then runs at
+        // least 3 passes (fewer leave nothing to overlap)
+        if (ctx->gemm_pipe && !kr_force && !ks_force) {
+            const uint32_t pp = (w->t32_chunks * F::CK + 255) / 256;
+            uint32_t pks = ((uint32_t)ctx->num_cus * 11 + 10 * tiles - 1) / (10 * tiles);
+            if (pks > pp) pks = pp;
+            if (pks < 1) pks = 1;
+            if ((pp + pks - 1) / pks >= 3) {
+                kr = 256;
+                ks = pks;
+                pipe = true;
+            }
+        } else if (ctx->gemm_pipe) {
+            pipe = true;   // forced shapes use it wherever there are several passes per workgroup
+        }
+    }
     if (kr_force) kr = kr_force;
     if (kr % (F::CK * KW) || kr * MT > 2048) return fail(ctx, JANUS_E_INVALID_DIM, "gemm: bad pass length");
     a.pass_chunks = kr / F::CK;
@@ -624,7 +816,7 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     a.chunks = w->t32_chunks;
     a.total_passes = (a.chunks + a.pass_chunks - 1) / a.pass_chunks;
     // split K over workgroups until there are about two workgroups per CU
-    uint32_t ks = (want + tiles - 1) / tiles;
+    if (!ks) ks = (want + tiles - 1) / tiles;
     if (ks_force) ks = ks_force;
     if (ks > a.total_passes) ks = a.total_passes;
     if (ks < 1) ks = 1;
@@ -650,8 +842,19 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
         attr_set = true;
     }
     const dim3 grid(tiles, a.ksplit), block(64 * WAVES * KW);
-    if (kr * MT <= 1024) hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, SPT1, PD>), grid, block, lds, ctx->stream, a);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, 2 * SPT1, PD>), grid, block, lds, ctx->stream, a);
+    // quantised weights: the cross-pass pipelined kernel for the usual pass lengths
+    bool piped = false;
+    if constexpr (!std::is_same<F, GF16>::value) {
+        if (pipe && a.passes_per_wg > 1) {
+            piped = true;
+            if (kr == 256) launch_pipe<F, MT, KW, 256>(ctx, grid, a);
+            else if (kr == 512) launch_pipe<F, MT, KW, 512>(ctx, grid, a);
+            else if (MT == 1 && kr == 1024) launch_pipe<F, MT, KW, 1024 / MT>(ctx, grid, a);
+            else piped = false;
+        }
+    }
+    if (!piped && kr * MT <= 1024) hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, SPT1, PD>), grid, block, lds, ctx->stream, a);
+    else if (!piped) hipLaunchKernelGGL((gemm_mfma_kernel<F, MT, KW, 2 * SPT1, PD>), grid, block, lds, ctx->stream, a);
     JANUS_LAUNCH_CHECK(ctx);
     if (parts) {
         parts->ws = a.ws;
@@ -868,7 +1071,7 @@ int gemm_swiglu(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t
         if (int e = mfma_gemm_prepare(ctx, w)) return e;
         GemmArgs g = make_args(w, a16, act16, 1, rows, nullptr);
         g.swiglu = 1;
-        return launch_mfma<GQ4_0, 1, 4, 2>(ctx, g, w, nullptr, 1024, 1);
+        return launch_mfma<GQ4_0, 1, 4, 2>(ctx, g, w, nullptr, ctx->gemm_pipe ? 512 : 1024, 1);
     }
     GemmPartials p{};
     if (int r = run_partials(ctx, a16, w, rows, &p)) return r;

@@ -168,6 +168,6 @@ def make_model(seed: int, hidden: int, heads: int, kv_heads: int, ffn: int, voca
 
 
 def tiny_config1(seed: int = 1) -> ModelSpec:
-    """2 layers, hidden 256, 4 heads x 64, 2 KV heads, FFN 688,
+    """benchmark configuration 1: 2 layers, hidden 256, 4 heads x 64, 2 KV heads, FFN 688,
     vocab 512, eps 1e-5, theta 1e4, Q8_0 blocks; ffn_down F32 because 688 % 32 != 0."""
     return make_model(seed, 256, 4, 2, 688, 512, 2, Q8_0, 1e-5, 10000.0, F32, F32, down_type=F32)

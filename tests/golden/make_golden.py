@@ -17,7 +17,7 @@ the same stored bytes from now on:
                 and hd 128 / theta 5e5 (model/transformer/constructor.rs:454-489).
   f16.npz       binary16 -> binary32 decodes of chosen bit patterns in the
                 three reference variants (exact, Q8_0 scale, flush-to-zero).
-  greedy_c1.npz BASELINE config 1 (synth.tiny_config1(1)): the 32-token prompt,
+  greedy_c1.npz benchmark configuration 1 (synth.tiny_config1(1)): the 32-token prompt,
                 the 16 greedy tokens under the reference loop and sampler
                 (generation.rs:129-323, sampler.rs:146-209) and the first
                 decode step's logits.

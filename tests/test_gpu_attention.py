@@ -4,7 +4,7 @@ Against the oracle (attention.wgsl:62-186 + softmax.wgsl:18-51 restated)
 with f32 K/V, and against the oracle fed binary16-rounded K/V for an f16
 cache; the invariant split-K == single pass is covered by lengths that span
 one and many splits. The ragged case packs sequences via a prefix-sum
-offset table into one launch (BASELINE config 4 shape, reduced lengths).
+offset table into one launch (benchmark configuration 4 shape, reduced lengths).
 """
 import numpy as np
 import pytest

@@ -65,6 +65,26 @@ def test_mfma_gemm_matches_stacked_gemv_and_f64(engine, ggml_type, rows, n, k):
     _check_against_f64(stacked.cpu().numpy(), wf, a16)
 
 
+@pytest.mark.parametrize("ggml_type", [2, 8, 12])
+@pytest.mark.parametrize("rows", [32, 48, 64])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336)])
+def test_pipelined_gemm_shapes_match_f64(engine, ggml_type, rows, n, k):
+    """Shapes whose workgroups run several K passes take the cross-pass
+    pipelined kernel (A double-buffered in LDS, next-pass weights in flight):
+    one and two 32-row M tiles, every quantised format, K split over
+    workgroups. Repeated calls are bitwise equal."""
+    raw, w = _weight(engine, ggml_type, n, k, 300 + ggml_type + rows)
+    a16 = _acts(rows, k, 7 * rows + n)
+    a = a16.to(DEV)
+    outs = []
+    for _ in range(2):
+        c = torch.empty(rows, n, device=DEV)
+        ops.gemm_auto(engine, a, w, c, rows, 1, k, n)
+        outs.append(c.cpu())
+    assert torch.equal(outs[0], outs[1])
+    _check_against_f64(outs[0].numpy(), w.dequant().cpu().numpy(), a16)
+
+
 @pytest.mark.parametrize("ggml_type", [2, 12])
 def test_mfma_gemm_is_deterministic_under_split_k(engine, ggml_type):
     n, k, rows = 4096, 4096, 32          # few row tiles: the product is split over K

@@ -124,7 +124,7 @@ def test_gemv_residual_epilogue(engine):
 
 @pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (4096, 4096)])
 def test_config2_q4_0_gemv_full_shapes(engine, n, k):
-    """Q4_0, x fp16 N(0,1), fp32 accumulate, fp16 output."""
+    """benchmark configuration 2: Q4_0, x fp16 N(0,1), fp32 accumulate, fp16 output."""
     rng = np.random.default_rng(2)
     raw = synth.random_q4_0(rng, n, k)
     w = ops.GpuTensor(engine, 2, n, k, raw)

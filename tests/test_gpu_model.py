@@ -1,4 +1,4 @@
-"""End-to-end parity of the decode driver on BASELINE config 1.
+"""End-to-end parity of the decode driver on benchmark configuration 1.
 
 Tiny random-init Llama (2 layers, hidden 256, 4 heads x 64, 2 KV heads,
 FFN 688, vocab 512, Q8_0 blocks, F32 ffn_down, eps 1e-5, theta 1e4):
