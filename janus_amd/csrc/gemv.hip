@@ -132,6 +132,7 @@ struct WPtr {
 // ---- Q4_0: 16 B nibbles (GGML order) + binary16 scale per 32 weights -------
 struct FQ4_0 {
     static constexpr int UNIT = 32;
+    static constexpr bool XREREAD = false;   // long rows re-read x from LDS per row group
     static constexpr bool PERM = true;
     struct W { uint4 q; uint16_t d; };
     __device__ static W load(WPtr w, size_t unit) {
@@ -229,6 +230,7 @@ struct FQ4_0 {
 // ---- Q8_0: 32 B int8 + binary16 scale (exp 31 -> 1e38) per 32 weights ------
 struct FQ8_0 {
     static constexpr int UNIT = 32;
+    static constexpr bool XREREAD = false;   // long rows re-read x from LDS per row group
     static constexpr bool PERM = true;
     struct W { uint4 q0, q1; uint16_t d; };
     __device__ static W load(WPtr w, size_t unit) {
@@ -283,6 +285,7 @@ struct FQ8_0 {
 // (shaders/gemm_q4_k.wgsl:82-113).
 struct FQ4_K {
     static constexpr int UNIT = 32;
+    static constexpr bool XREREAD = true;   // long rows re-read x from LDS per row group
     static constexpr bool PERM = true;
     // The 16-byte super-block header (d, dmin, 12 scale bytes) is shared by
     // the 8 units of a super-block, which sit on 8 consecutive lanes in every
@@ -366,19 +369,17 @@ struct FQ4_K {
         r.c = c;
         return r;
     }
-    // (sc, m) pair of sub-block `sub` from the 12 scale bytes held in hdr.y..w.
+    // (sc, m) pair of sub-block `sub` from the 12 scale bytes held in hdr.y..w
+    // (bytes 0-3, 4-7, 8-11). `sub` differs between lanes, so both forms are
+    // computed and selected: a branch would run both under exec masks.
     __device__ static void scale_min(const uint4 &hdr, int sub, float &sc, float &mn) {
-        uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;   // bytes 0-3, 4-7, 8-11
-        uint32_t scv, mnv;
-        if (sub < 4) {
-            scv = (s0 >> (8 * sub)) & 63u;
-            mnv = (s1 >> (8 * sub)) & 63u;
-        } else {
-            int i = sub - 4;
-            uint32_t b8 = (s2 >> (8 * i)) & 0xffu;
-            scv = (b8 & 15u) | (((s0 >> (8 * i)) & 0xffu) >> 6 << 4);
-            mnv = (b8 >> 4) | (((s1 >> (8 * i)) & 0xffu) >> 6 << 4);
-        }
+        const uint32_t sh = 8u * (uint32_t)(sub & 3);
+        const uint32_t b0 = hdr.y >> sh, b1 = hdr.z >> sh, b2 = hdr.w >> sh;
+        const bool low = sub < 4;
+        // sub < 4: low 6 bits of byte sub of s0 / s1; else the nibbles of byte
+        // sub - 4 of s2 with bits 6-7 of byte sub - 4 of s0 / s1 on top
+        const uint32_t scv = low ? (b0 & 63u) : ((b2 & 15u) | ((b0 >> 2) & 48u));
+        const uint32_t mnv = low ? (b1 & 63u) : (((b2 >> 4) & 15u) | ((b1 >> 2) & 48u));
         sc = (float)scv;
         mn = (float)mnv;
     }
@@ -439,6 +440,7 @@ struct FQ4_K {
 // ---- F16 weights: a unit is 8 binary16 weights (one 16-byte load) ----------
 struct FF16 {
     static constexpr int UNIT = 8;
+    static constexpr bool XREREAD = false;   // long rows re-read x from LDS per row group
     static constexpr bool PERM = false;
     struct W { uint4 q; };
     __device__ static W load(WPtr w, size_t unit) {
@@ -722,13 +724,23 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             XR xv;
-            if constexpr (XMODE == 2) xv = F::loadx(xs, sx16, uu[i]);
-            else xv = xr[i];
+            if constexpr (XMODE == 2) {
+                int u = uu[i];
+                // Q4_K: x does not change between row groups and the compiler
+                // would hoist every unit's read out of the group loop, keeping
+                // them all live (spills on long rows); an opaque index keeps
+                // each read next to its use
+                if constexpr (F::XREREAD) asm volatile("" : "+v"(u));
+                xv = F::loadx(xs, sx16, u);
+            } else {
+                xv = xr[i];
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float d = F::dot(w[i][r], xv);
                 acc[r] = ok[i] ? acc[r] + d : acc[r];
             }
+            if constexpr (XMODE == 2 && F::XREREAD) __builtin_amdgcn_sched_barrier(0);
         }
         int ridx;
         float s = reduce_wave_rows<R>(acc, lane, ridx);
