@@ -279,19 +279,22 @@ int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vo
     return JANUS_OK;
 }
 
-// Each workgroup scans 8192 logits of one row (8 float4 per thread, all loads
-// in flight together) and each wavefront posts one atomicMax of its best key.
-__global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restrict__ logits,
-                                                          unsigned long long *best, uint32_t vocab) {
+// Each 1024-thread workgroup scans 32768 logits of one row (8 float4 per
+// thread, all loads in flight together), reduces its keys through LDS and
+// posts one atomicMax: a row's slot takes one device-scope atomic per
+// workgroup (4 for a 128k vocabulary) rather than one per wavefront.
+__global__ __launch_bounds__(1024) void argmax_keys_kernel(const float *__restrict__ logits,
+                                                           unsigned long long *best, uint32_t vocab) {
+    __shared__ uint64_t wbest[16];
     const uint32_t row = blockIdx.y;
     const float *l = logits + (size_t)row * vocab;
-    const uint32_t base = blockIdx.x * 8192u + threadIdx.x * 4u;
+    const uint32_t base = blockIdx.x * 32768u + threadIdx.x * 4u;
     uint64_t key = 0;
     float4 v[8];
     const bool vec = (vocab & 3u) == 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const uint32_t i = base + 1024u * j;
+        const uint32_t i = base + 4096u * j;
         if (vec && i + 4 <= vocab) {
             v[j] = *(const float4 *)(l + i);
         } else {
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restric
     };
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const uint32_t i = base + 1024u * j;
+        const uint32_t i = base + 4096u * j;
         take(v[j].x, i);
         take(v[j].y, i + 1);
         take(v[j].z, i + 2);
@@ -321,13 +324,19 @@ __global__ __launch_bounds__(256) void argmax_keys_kernel(const float *__restric
                                (uint32_t)shfl_xor((int)(key & 0xffffffffu), o);
         key = other > key ? other : key;
     }
-    if ((threadIdx.x & 63) == 0 && key) atomicMax(best + row, (unsigned long long)key);
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t k = 0;
+        for (int w = 0; w < 16; ++w) k = wbest[w] > k ? wbest[w] : k;
+        if (k) atomicMax(best + row, (unsigned long long)k);
+    }
 }
 
 int argmax_keys_launch(janus_ctx *ctx, const float *logits, unsigned long long *best, uint32_t vocab,
                        uint32_t batch) {
-    hipLaunchKernelGGL(argmax_keys_kernel, dim3((vocab + 8191) / 8192, batch), dim3(256), 0, ctx->stream, logits, best,
-                       vocab);
+    hipLaunchKernelGGL(argmax_keys_kernel, dim3((vocab + 32767) / 32768, batch), dim3(1024), 0, ctx->stream, logits,
+                       best, vocab);
     JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
 }
