@@ -85,6 +85,22 @@ def test_pipelined_gemm_shapes_match_f64(engine, ggml_type, rows, n, k):
     _check_against_f64(outs[0].numpy(), w.dequant().cpu().numpy(), a16)
 
 
+@pytest.mark.parametrize("ggml_type", [2, 8])
+@pytest.mark.parametrize("rows", [32, 40])
+def test_pipelined_gemm_ragged_k_and_partial_tile(engine, ggml_type, rows):
+    """k = 4160 leaves a 64-wide last pass (K-tail chunks clamped, not computed)
+    and n = 6176 leaves a last tile with one active row group of four (the
+    others stream a real group and discard it)."""
+    n, k = 6176, 4160
+    raw, w = _weight(engine, ggml_type, n, k, 500 + ggml_type + rows)
+    a16 = _acts(rows, k, 11 * rows)
+    a = a16.to(DEV)
+    c = torch.empty(rows, n, device=DEV)
+    ops.gemm_auto(engine, a, w, c, rows, 1, k, n)
+    torch.cuda.synchronize()
+    _check_against_f64(c.cpu().numpy(), w.dequant().cpu().numpy(), a16)
+
+
 @pytest.mark.parametrize("ggml_type", [2, 12])
 def test_mfma_gemm_is_deterministic_under_split_k(engine, ggml_type):
     n, k, rows = 4096, 4096, 32          # few row tiles: the product is split over K
