@@ -760,7 +760,7 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
-        hipFree(mem);
+        (void)hipFree(mem);   // already failing: the repack error is the one reported
         return hip_fail(ctx, e, "t32 repack");
     }
     w->t32 = mem;

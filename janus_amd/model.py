@@ -12,10 +12,10 @@ from typing import Sequence
 
 import numpy as np
 
-from . import _lib
-from ._lib import DT_F16, DT_F32, ModelConfig, check
+from . import _lib, gguf, ops
+from ._lib import DT_F16, DT_F32, DT_Q4_0, DT_Q4_K, DT_Q8_0, ModelConfig, check
 from .ops import ComputeEngine
-from .synth import ModelSpec
+from .synth import ModelSpec, Tensor
 
 
 class Model:
@@ -35,6 +35,32 @@ class Model:
             self._check(self.lib.janus_model_set_tensor(h, t.name.encode(), t.ggml_type, t.n, t.k,
                                                         buf.ctypes.data, buf.nbytes))
         self._check(self.lib.janus_model_validate(h))
+
+    @classmethod
+    def from_gguf(cls, engine: ComputeEngine, path, max_seq_len: int | None = None, max_batch: int = 1,
+                  kv_dtype: int = DT_F32, act_dtype: int = DT_F32) -> "Model":
+        """Model::new from a GGUF file (model/transformer/constructor.rs:23-437):
+        the config from the file's metadata (model/config.rs:377-446; max_seq_len
+        defaults to its clamped context_length) and every tensor handed to the
+        weight upload as the file stores it, read through the memory map.
+
+        A quantised token_embd.weight (Q4_0 / Q8_0 / Q4_K) becomes a binary16
+        table as allocate_tensors does (compute/engine.rs:635-771), but in GGML
+        element order for every format: the blocks are dequantised on the GPU by
+        the weight upload's closed form and rounded to binary16 (RNE). The
+        reference's own Q4_K embedding path uses a non-GGML order
+        (engine.rs:267-316) and is not followed."""
+        f = gguf.GgufFile(path)
+        try:
+            c = gguf.config_from_metadata(f.meta.metadata)
+            m = cls(engine, ModelSpec(c.hidden, c.heads, c.kv_heads, c.ffn, c.vocab, c.layers, c.rms_eps,
+                                      c.rope_theta, [_gguf_tensor(engine, f, t) for t in f.tensors]),
+                    max_seq_len or c.max_seq_len, max_batch, kv_dtype, act_dtype)
+            # the weights are uploaded: drop the views into the mapping
+            m.spec = ModelSpec(c.hidden, c.heads, c.kv_heads, c.ffn, c.vocab, c.layers, c.rms_eps, c.rope_theta)
+            return m
+        finally:
+            f.close()
 
     def _check(self, status: int) -> None:
         check(status, self.engine.ctx)
@@ -92,3 +118,21 @@ class Model:
 
     def kv_cache_ptr(self, which: int) -> int:
         return self.lib.janus_model_kv_cache(self.handle, which)
+
+
+def _gguf_tensor(engine: ComputeEngine, f, t) -> Tensor:
+    n, k = t.shape_nk()
+    if t.name == "token_embd.weight" and t.ggml_type in (DT_Q4_0, DT_Q8_0, DT_Q4_K):
+        return Tensor(t.name, DT_F16, n, k, _embedding_f16(engine, t.ggml_type, n, k, f.tensor_data(t)))
+    return Tensor(t.name, t.ggml_type, n, k, f.tensor_data(t))
+
+
+def _embedding_f16(engine: ComputeEngine, ggml_type: int, n: int, k: int, raw) -> np.ndarray:
+    """Quantised embedding blocks -> binary16 [n][k] (GGML element order): the
+    GPU weight dequant's exact f32 values, rounded to nearest-even binary16."""
+    w = ops.GpuTensor(engine, ggml_type, n, k, raw)
+    try:
+        h = w.dequant().half().cpu().numpy()
+    finally:
+        w.free()
+    return h.view(np.uint16)

@@ -171,3 +171,22 @@ def tiny_config1(seed: int = 1) -> ModelSpec:
     """benchmark configuration 1: 2 layers, hidden 256, 4 heads x 64, 2 KV heads, FFN 688,
     vocab 512, eps 1e-5, theta 1e4, Q8_0 blocks; ffn_down F32 because 688 % 32 != 0."""
     return make_model(seed, 256, 4, 2, 688, 512, 2, Q8_0, 1e-5, 10000.0, F32, F32, down_type=F32)
+
+
+def write_gguf(spec: ModelSpec, path, context_length: int = 4096, alignment: int = 32) -> None:
+    """Write a spec as a Llama-architecture GGUF file: the metadata keys
+    model_config_from_gguf_metadata reads (model/config.rs:377-446) and every
+    tensor with its dimensions innermost first ([k, n] for a 2-D [n][k] weight)."""
+    from . import gguf as G
+    md = {"general.architecture": G.Value(G.STRING, "llama"),
+          "llama.embedding_length": G.Value(G.UINT32, spec.hidden),
+          "llama.block_count": G.Value(G.UINT32, spec.layers),
+          "llama.attention.head_count": G.Value(G.UINT32, spec.heads),
+          "llama.attention.head_count_kv": G.Value(G.UINT32, spec.kv_heads),
+          "llama.feed_forward_length": G.Value(G.UINT32, spec.ffn),
+          "llama.context_length": G.Value(G.UINT32, context_length),
+          "llama.attention.layer_norm_rms_epsilon": G.Value(G.FLOAT32, spec.rms_eps),
+          "llama.rope.freq_base": G.Value(G.FLOAT32, spec.rope_theta),
+          "llama.vocab_size": G.Value(G.UINT32, spec.vocab)}
+    tensors = [(t.name, [t.k, t.n] if t.k else [t.n], t.ggml_type, t.data) for t in spec.tensors]
+    G.write(path, md, tensors, alignment=alignment)
