@@ -52,13 +52,18 @@ typedef enum janus_dtype {
     JANUS_DT_F16 = 1,
     JANUS_DT_Q4_0 = 2,
     JANUS_DT_Q8_0 = 8,
-    JANUS_DT_Q4_K = 12
+    JANUS_DT_Q4_K = 12,
+    JANUS_DT_Q5_K = 13,
+    JANUS_DT_Q6_K = 14
 } janus_dtype;
 
 /* janus_weight_upload flags. */
 #define JANUS_WEIGHT_FTZ_F16 0x1u  /* decode binary16 values (F16 weights, Q4_K d/dmin)
                                       with f16_to_f32_safe semantics: subnormals -> +-0
                                       (shaders/gemm_q4_k.wgsl:30-43, shaders/gemm.wgsl:18-31) */
+#define JANUS_WEIGHT_Q6K_REF_ORDER 0x2u  /* Q6_K: the element order of the reference loader's
+                                            q6_k_to_f32 (compute/engine.rs:198-248) instead of
+                                            GGML's dequantize_row_q6_K order */
 
 /* argmax tie rules. */
 #define JANUS_TIE_LAST 0  /* Sampler::argmax, model/sampler.rs:784-795: last maximal index */
@@ -96,9 +101,14 @@ int janus_d2h(janus_ctx *ctx, void *h_dst, const void *d_src, size_t bytes); /* 
  *   Q4_0 -> 18-byte GGML blocks (no reference kernel: engine.rs:833-838);
  *   Q8_0 -> 34-byte GGML blocks (engine.rs:772-797, read with the GGML
  *           34-byte stride rather than the shader's 36, gemm_q8_0.wgsl:79);
- *   Q4_K -> 144-byte GGML block_q4_K (engine.rs:662-687).
+ *   Q4_K -> 144-byte GGML block_q4_K (engine.rs:662-687);
+ *   Q5_K -> 176-byte GGML block_q5_K, kept raw as the reference keeps it
+ *           (engine.rs:717-742) but read in GGML order (its shader,
+ *           gemm_q5_k.wgsl:6-23, reads the bytes at other offsets);
+ *   Q6_K -> 210-byte GGML block_q6_K, dequantised on the host to binary16
+ *           exactly as engine.rs:800-831 does; the handle then reports F16.
  * The library repacks into its own HBM layout. k must be a multiple of the
- * block width (32, or 256 for Q4_K): JANUS_E_INVALID_DIM otherwise. */
+ * block width (32, or 256 for the K-quants): JANUS_E_INVALID_DIM otherwise. */
 int janus_weight_upload(janus_ctx *ctx, int ggml_type, uint32_t n, uint32_t k,
                         const void *bytes, size_t nbytes, uint32_t flags,
                         janus_weight **out);

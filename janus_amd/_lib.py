@@ -28,8 +28,11 @@ DT_F16 = 1
 DT_Q4_0 = 2
 DT_Q8_0 = 8
 DT_Q4_K = 12
+DT_Q5_K = 13
+DT_Q6_K = 14
 
 WEIGHT_FTZ_F16 = 0x1
+WEIGHT_Q6K_REF_ORDER = 0x2
 TIE_LAST = 0
 TIE_WGSL = 1
 

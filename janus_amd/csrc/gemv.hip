@@ -305,7 +305,7 @@ struct FQ4_K {
     template <int T> __device__ static uint32_t quad_word(uint32_t v) {
         return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, T * 0x55, 0xf, 0xf, false);   // quad_perm [T,T,T,T]
     }
-    __device__ static uint4 header(const W &w) {
+    template <class WW> __device__ static uint4 header(const WW &w) {
         return make_uint4(quad_word<0>(w.hw), quad_word<1>(w.hw), quad_word<2>(w.hw), quad_word<3>(w.hw));
     }
     // x for one chunk: 16 low-nibble elements and 16 high-nibble elements.
@@ -383,8 +383,8 @@ struct FQ4_K {
         sc = (float)scv;
         mn = (float)mnv;
     }
-    template <class X>
-    __device__ static float finish(const W &w, const X &x, float qlo, float qhi) {
+    template <class WW, class X>
+    __device__ static float finish(const WW &w, const X &x, float qlo, float qhi) {
         const uint4 hdr = header(w);
         float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
         int j = x.c >> 1;
@@ -434,6 +434,73 @@ struct FQ4_K {
             h1 = dot2(e, x.hi[2 * i + 1], h1);
         }
         return finish(w, x, l0 + l1, (h0 + h1) * 0.0625f);
+    }
+};
+
+// ---- Q5_K: GGML 176-byte super-blocks {d, dmin, scales[12], qh[32], qs[128]} --
+// Same header, sub-block scales and element order as Q4_K (a unit is one
+// 16-byte chunk of qs, x layout shared), plus a fifth bit per element: chunk
+// c = 2j + h covers qh bytes 16h..16h+15, bit 2j for the low nibbles and bit
+// 2j + 1 for the high ones (ggml-quants.c dequantize_row_q5_K). Weight =
+// (d*sc)*q - dmin*m with q in 0..31.
+struct FQ5_K : FQ4_K {
+    struct W { uint4 q; uint4 qh; uint32_t hw; };
+    __device__ static W load(WPtr w, size_t unit) {
+        size_t sb = unit >> 3;
+        int c = (int)(unit & 7);
+        const uint4 *blk = (const uint4 *)(w.qs + sb * 176);
+        W r;
+        r.hw = ((const uint32_t *)blk)[__lane_id() & 3];
+        r.qh = ld_stream(blk + 1 + (c & 1));
+        r.q = ld_stream(blk + 3 + c);
+        return r;
+    }
+    // 5-bit values of the four bytes of q word i: low (lo) and high (hi) elements
+    __device__ static void q5(const W &w, int i, int j, uint32_t &lo, uint32_t &hi) {
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        const uint32_t h[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        const uint32_t hb = h[i] >> (2 * j);
+        lo = (q[i] & 0x0f0f0f0fu) | ((hb & 0x01010101u) << 4);
+        hi = ((q[i] >> 4) & 0x0f0f0f0fu) | ((hb & 0x02020202u) << 3);
+    }
+    __device__ static float dot(const W &w, const XF &x) {
+        const int j = x.c >> 1;
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo, hi;
+            q5(w, i, j, lo, hi);
+            l0 = fmaf(cvt_b0(lo), x.lo[i].x, l0);
+            l1 = fmaf(cvt_b1(lo), x.lo[i].y, l1);
+            l0 = fmaf(cvt_b2(lo), x.lo[i].z, l0);
+            l1 = fmaf(cvt_b3(lo), x.lo[i].w, l1);
+            h0 = fmaf(cvt_b0(hi), x.hi[i].x, h0);
+            h1 = fmaf(cvt_b1(hi), x.hi[i].y, h1);
+            h0 = fmaf(cvt_b2(hi), x.hi[i].z, h0);
+            h1 = fmaf(cvt_b3(hi), x.hi[i].w, h1);
+        }
+        return finish(w, x, l0 + l1, h0 + h1);
+    }
+    __device__ static float dot(const W &w, const XH &x) {
+        const int j = x.c >> 1;
+        const jh2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const uint32_t m = vgpr_const_6400();
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo, hi;
+            q5(w, i, j, lo, hi);
+            // bytes 0, 2 and 1, 3 of each word as binary16 1024 + q (q <= 31 is exact)
+            jh2 a = as_h2((lo & 0x001f001fu) | m) - off;
+            jh2 c = as_h2(((lo >> 8) & 0x001f001fu) | m) - off;
+            jh2 b = as_h2((hi & 0x001f001fu) | m) - off;
+            jh2 e = as_h2(((hi >> 8) & 0x001f001fu) | m) - off;
+            l0 = dot2(a, x.lo[2 * i], l0);
+            l1 = dot2(c, x.lo[2 * i + 1], l1);
+            h0 = dot2(b, x.hi[2 * i], h0);
+            h1 = dot2(e, x.hi[2 * i + 1], h1);
+        }
+        return finish(w, x, l0 + l1, h0 + h1);
     }
 };
 
@@ -1213,6 +1280,7 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
     case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, norm, true, done); break;
     case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, norm, true, done); break;
     case JANUS_DT_Q4_K: a.units = w->k / 32; e = launch_lds_fmt<FQ4_K>(ctx, a, norm, true, done); break;
+    case JANUS_DT_Q5_K: a.units = w->k / 32; e = launch_lds_fmt<FQ5_K>(ctx, a, norm, true, done); break;
     case JANUS_DT_F16:
         if (w->k % 8) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: F16 rows need k % 8 == 0");
         a.units = w->k / 8;
@@ -1245,6 +1313,7 @@ int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float
     case JANUS_DT_Q4_0: a.units = w->k / 32; e = launch_lds_fmt<FQ4_0>(ctx, a, true, false, done); break;
     case JANUS_DT_Q8_0: a.units = w->k / 32; e = launch_lds_fmt<FQ8_0>(ctx, a, true, false, done); break;
     case JANUS_DT_Q4_K: a.units = w->k / 32; e = launch_lds_fmt<FQ4_K>(ctx, a, true, false, done); break;
+    case JANUS_DT_Q5_K: a.units = w->k / 32; e = launch_lds_fmt<FQ5_K>(ctx, a, true, false, done); break;
     case JANUS_DT_F16:
         if (w->k % 8) return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: F16 rows need k % 8 == 0");
         a.units = w->k / 8;
@@ -1273,6 +1342,7 @@ int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w
     case JANUS_DT_Q4_0: a.units = w->k / 32; return launch_gemv<FQ4_0>(ctx, a, x_dt);
     case JANUS_DT_Q8_0: a.units = w->k / 32; return launch_gemv<FQ8_0>(ctx, a, x_dt);
     case JANUS_DT_Q4_K: a.units = w->k / 32; return launch_gemv<FQ4_K>(ctx, a, x_dt);
+    case JANUS_DT_Q5_K: a.units = w->k / 32; return launch_gemv<FQ5_K>(ctx, a, x_dt);
     case JANUS_DT_F16:
         if (w->k % 8 == 0) {
             a.units = w->k / 8;

@@ -411,7 +411,8 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
                                                       std::to_string(cols) + "]");
         // 2-D float weights follow allocate_tensors: binary16 storage decoded with
         // f16_to_f32_safe (shaders/gemm.wgsl:18-31, embed.wgsl:11-20).
-        if (type == JANUS_DT_F32 || type == JANUS_DT_F16) flags |= JANUS_WEIGHT_FTZ_F16;
+        // Q6_K is loaded as binary16 (engine.rs:800-831) and takes the same path.
+        if (type == JANUS_DT_F32 || type == JANUS_DT_F16 || type == JANUS_DT_Q6_K) flags |= JANUS_WEIGHT_FTZ_F16;
         if (type == JANUS_DT_Q4_K) flags |= JANUS_WEIGHT_FTZ_F16;   // gemm_q4_k.wgsl:62-65
         janus_weight *w = nullptr;
         if (int e = janus_weight_upload(ctx, type, n, k, bytes, nbytes, flags, &w)) return e;
@@ -427,16 +428,17 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
         janus_weight_free(ctx, L.gu);
         L.qkv = L.gu = nullptr;
     }
+    // Q6_K tensors arrive as binary16 whatever their role (engine.rs:800-831).
     if (name == "token_embd.weight") {
-        if (type != JANUS_DT_F32 && type != JANUS_DT_F16)
-            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "token_embd.weight must be F32 or F16");
+        if (type != JANUS_DT_F32 && type != JANUS_DT_F16 && type != JANUS_DT_Q6_K)
+            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "token_embd.weight must be F32, F16 or Q6_K");
         return set_w(&m->tok_embd, c.vocab, c.hidden, 0);
     }
     if (name == "output_norm.weight") return set_vec(&m->out_norm, c.hidden);
     if (name == "output.weight") {
         // The LM head is always the f16 GEMM (model/transformer/forward.rs:101-111).
-        if (type != JANUS_DT_F32 && type != JANUS_DT_F16)
-            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "output.weight must be F32 or F16");
+        if (type != JANUS_DT_F32 && type != JANUS_DT_F16 && type != JANUS_DT_Q6_K)
+            return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "output.weight must be F32, F16 or Q6_K");
         return set_w(&m->lm_head, c.vocab, c.hidden, 0);
     }
     uint32_t l;

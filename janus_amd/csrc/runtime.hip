@@ -60,6 +60,7 @@ size_t weight_qs_row_bytes(int type, uint32_t k) {
     case JANUS_DT_Q4_0: return (size_t)k / 32 * 16;
     case JANUS_DT_Q8_0: return (size_t)k / 32 * 32;
     case JANUS_DT_Q4_K: return (size_t)k / 256 * 144;
+    case JANUS_DT_Q5_K: return (size_t)k / 256 * 176;
     case JANUS_DT_F16: return (size_t)k * 2;
     default: return 0;
     }
@@ -170,6 +171,33 @@ __global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ blocks, float *_
             uint8_t byte = blk[16 + 32 * j + t];
             out[b * 256 + 64 * j + t] = scale_lo * (float)(byte & 15) - min_lo;
             out[b * 256 + 64 * j + 32 + t] = scale_hi * (float)(byte >> 4) - min_hi;
+        }
+    }
+}
+
+// Q5_K (GGML block_q5_K): the Q4_K form with a fifth bit per element, bit 2j
+// (low nibbles) or 2j + 1 (high nibbles) of qh[t]. (d*sc)*q is exact in
+// binary32 (11 + 6 + 5 bits), so the one rounding is the difference.
+__global__ void dequant_q5_k_kernel(const uint8_t *__restrict__ blocks, float *__restrict__ out,
+                                    size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t *blk = blocks + b * 176;
+    float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    float dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
+    const uint8_t *qh = blk + 16, *qs = blk + 48;
+    for (int j = 0; j < 4; ++j) {
+        int sl, ml, sh, mh;
+        q4k_scale_min(blk + 4, 2 * j, sl, ml);
+        q4k_scale_min(blk + 4, 2 * j + 1, sh, mh);
+        float scale_lo = d * (float)sl, min_lo = dmin * (float)ml;
+        float scale_hi = d * (float)sh, min_hi = dmin * (float)mh;
+        for (int t = 0; t < 32; ++t) {
+            const uint8_t byte = qs[32 * j + t];
+            const int lo = (byte & 15) | (((qh[t] >> (2 * j)) & 1) << 4);
+            const int hi = (byte >> 4) | (((qh[t] >> (2 * j + 1)) & 1) << 4);
+            out[b * 256 + 64 * j + t] = scale_lo * (float)lo - min_lo;
+            out[b * 256 + 64 * j + 32 + t] = scale_hi * (float)hi - min_hi;
         }
     }
 }
@@ -370,21 +398,74 @@ int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const 
         }
         break;
     }
-    case JANUS_DT_Q4_K: {
+    case JANUS_DT_Q4_K:
+    case JANUS_DT_Q5_K: {
+        const bool q5 = type == JANUS_DT_Q5_K;
+        const size_t bb = q5 ? 176 : 144;
         if (k % 256) return fail(ctx, JANUS_E_INVALID_DIM,
-                                 "Q4_K gemm requires cols to be multiple of 256, got " + std::to_string(k));
+                                 std::string(q5 ? "Q5_K" : "Q4_K") +
+                                     " gemm requires cols to be multiple of 256, got " + std::to_string(k));
         size_t nblk = elems / 256;
-        if (nbytes != nblk * 144) return fail(ctx, JANUS_E_INVALID_DIM, "Q4_K tensor byte size mismatch");
+        if (nbytes != nblk * bb) return fail(ctx, JANUS_E_INVALID_DIM, "K-quant tensor byte size mismatch");
         qs.assign(src, src + nbytes);
         if (ftz)
             for (size_t b = 0; b < nblk; ++b) {
-                uint8_t *blk = qs.data() + b * 144;
+                uint8_t *blk = qs.data() + b * bb;
                 for (int o = 0; o < 4; o += 2) {
                     uint16_t h = ftz16(rd16(blk + o));
                     blk[o] = (uint8_t)(h & 0xff);
                     blk[o + 1] = (uint8_t)(h >> 8);
                 }
             }
+        break;
+    }
+    case JANUS_DT_Q6_K: {
+        // The reference dequantises Q6_K on the host and keeps binary16
+        // weights (engine.rs:800-831); so does this upload, in GGML element
+        // order or, with JANUS_WEIGHT_Q6K_REF_ORDER, in q6_k_to_f32's
+        // (engine.rs:198-248). Both form (d * scale) * (q - 32) in binary32
+        // and round to binary16 to nearest even.
+        if (k % 256) return fail(ctx, JANUS_E_INVALID_DIM,
+                                 "Q6_K requires cols to be multiple of 256, got " + std::to_string(k));
+        size_t nblk = elems / 256;
+        if (nbytes != nblk * 210)
+            return fail(ctx, JANUS_E_INVALID_DIM,
+                        "Q6_K tensor byte size " + std::to_string(nbytes) + " is not " + std::to_string(nblk) +
+                            " blocks of 210");
+        const bool ref_order = (flags & JANUS_WEIGHT_Q6K_REF_ORDER) != 0;
+        qs.resize(elems * 2);
+        uint16_t *dst = (uint16_t *)qs.data();
+        for (size_t b = 0; b < nblk; ++b) {
+            const uint8_t *blk = src + b * 210, *ql = blk, *qh = blk + 128;
+            const int8_t *sc = (const int8_t *)(blk + 192);
+            _Float16 dh;
+            uint16_t dbits = rd16(blk + 208);
+            std::memcpy(&dh, &dbits, 2);
+            const float d = (float)dh;
+            uint16_t *o = dst + b * 256;
+            for (int i = 0; i < 256; ++i) {
+                int q, s;
+                if (ref_order) {
+                    const unsigned lo = (i & 1) ? (ql[i / 2] >> 4) : (ql[i / 2] & 15u);
+                    const unsigned hi = (qh[i / 4] >> (2 * (i % 4))) & 3u;
+                    q = (int)((hi << 4) | lo) - 32;
+                    s = sc[i / 16];
+                } else {
+                    // element i = 128 h + 32 p + l: ql byte 64 h + l (+ 32 for p odd),
+                    // nibble p / 2, qh byte 32 h + l bits 2 p, scale 8 h + l / 16 + 2 p
+                    const int h = i >> 7, p = (i >> 5) & 3, l = i & 31;
+                    const uint8_t qlb = ql[64 * h + l + ((p & 1) ? 32 : 0)];
+                    const unsigned lo = (p & 2) ? (qlb >> 4) : (qlb & 15u);
+                    const unsigned hi = (qh[32 * h + l] >> (2 * p)) & 3u;
+                    q = (int)((hi << 4) | lo) - 32;
+                    s = sc[8 * h + l / 16 + 2 * p];
+                }
+                const float v = d * (float)s * (float)q;
+                const uint16_t hb = f32_to_f16_host(v);
+                o[i] = ftz ? ftz16(hb) : hb;
+            }
+        }
+        type = JANUS_DT_F16;
         break;
     }
     default:
@@ -447,6 +528,11 @@ int janus_weight_dequant(janus_ctx *ctx, const janus_weight *w, float *d_out) {
     case JANUS_DT_Q4_K: {
         size_t nb = elems / 256;
         dequant_q4_k_kernel<<<(unsigned)((nb + T - 1) / T), T, 0, ctx->stream>>>(w->qs, d_out, nb);
+        break;
+    }
+    case JANUS_DT_Q5_K: {
+        size_t nb = elems / 256;
+        dequant_q5_k_kernel<<<(unsigned)((nb + T - 1) / T), T, 0, ctx->stream>>>(w->qs, d_out, nb);
         break;
     }
     case JANUS_DT_F16:

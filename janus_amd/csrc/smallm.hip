@@ -231,6 +231,51 @@ struct GQ4_K {
     }
 };
 
+// Q5_K (GGML block_q5_K): the T32 copy holds each 5-bit value as a byte in
+// the Q8_0 chunk order and, per (row, 32-element sub-block), the pair
+// (d*sc, dmin*m) in binary32; w = (d*sc)*q - dmin*m as for Q4_K, the m term
+// from the staged activation sums.
+struct GQ5_K {
+    static constexpr int CK = 32;
+    struct W { uint4 q; float2 s; };
+    __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
+        const size_t ch = (size_t)g * a.chunks + c;
+        W w;
+        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
+        w.s = ((const float2 *)a.side)[ch * 32 + (lane & 31)];
+        return w;
+    }
+    template <int MT>
+    __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                               const float *Ss, uint32_t, f16x (&acc)[MT]) {
+        const int h = lane >> 5, r = lane & 31;
+        const h8 b0 = unpack_i8x8(w.q.x, w.q.y);
+        const h8 b1 = unpack_i8x8(w.q.z, w.q.w);
+        const float ds = w.s.x, dm = w.s.y;
+        const uint32_t sub = kl / 32;   // sub-block index within the pass
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + 8 * h;
+            f16x t = mfma(lds_h8(ap), b0, (f16x){});
+            t = mfma(lds_h8(ap + 16), b1, t);
+            const float *sx = Ss + (size_t)sub * (MT * 32) + mt * 32 + 4 * h;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const jf4 s4 = *(const jf4 *)(sx + 8 * jj);
+                acc[mt][4 * jj + 0] = fmaf(-dm, s4.x, fmaf(ds, t[4 * jj + 0], acc[mt][4 * jj + 0]));
+                acc[mt][4 * jj + 1] = fmaf(-dm, s4.y, fmaf(ds, t[4 * jj + 1], acc[mt][4 * jj + 1]));
+                acc[mt][4 * jj + 2] = fmaf(-dm, s4.z, fmaf(ds, t[4 * jj + 2], acc[mt][4 * jj + 2]));
+                acc[mt][4 * jj + 3] = fmaf(-dm, s4.w, fmaf(ds, t[4 * jj + 3], acc[mt][4 * jj + 3]));
+            }
+        }
+    }
+};
+
+// formats whose mins need the per-(row, sub-block) activation sums in LDS
+template <class F> struct NeedsSums { static constexpr bool value = false; };
+template <> struct NeedsSums<GQ4_K> { static constexpr bool value = true; };
+template <> struct NeedsSums<GQ5_K> { static constexpr bool value = true; };
+
 struct GF16 {
     static constexpr int CK = 16;
     struct W { uint4 q; };
@@ -305,7 +350,7 @@ __device__ __forceinline__ void store_swiglu(const GemmArgs &a, uint32_t g, int 
 template <class F, int MT, int KW, int SPT, int PD = Stage<F>::PD>
 __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
+    constexpr bool SUMS = NeedsSums<F>::value;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rgw = wave % WAVES, kw = wave / WAVES;   // row group in the tile, K slice of the pass
     const uint32_t G = (a.n + 31) / 32;
@@ -432,7 +477,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
 template <class F, int MT, int KW, int KR>
 __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr bool SUMS = std::is_same<F, GQ4_K>::value;
+    constexpr bool SUMS = NeedsSums<F>::value;
     constexpr int NT = 64 * WAVES * KW;   // threads
     constexpr int PC = KR / F::CK;        // chunks per pass
     constexpr int CPW = PC / KW;          // chunks per wavefront per pass
@@ -575,7 +620,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) 
 template <class F, int MT, int KW, int KR>
 constexpr size_t pipe_lds() {
     constexpr size_t abytes = (size_t)MT * 32 * (KR + 8) * 2;
-    constexpr size_t buf = (abytes + (std::is_same<F, GQ4_K>::value ? (size_t)(KR / 32) * MT * 32 * 4 : 0) + 15) / 16 * 16;
+    constexpr size_t buf = (abytes + (NeedsSums<F>::value ? (size_t)(KR / 32) * MT * 32 * 4 : 0) + 15) / 16 * 16;
     constexpr size_t red = (size_t)WAVES * KW * 16 * 64 * 4;
     return 2 * buf > red ? 2 * buf : red;
 }
@@ -674,6 +719,45 @@ __global__ void t32_q4_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq,
     if (lane < 32 && j == 0) *(uint4 *)(dside + (((size_t)g * (C / 4) + sb) * 32 + lane) * 16) = hdr;
 }
 
+__global__ void t32_q5_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq, float2 *dside, uint32_t n,
+                                uint32_t k, uint32_t G, uint32_t C) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)G * C * 64) return;
+    const int lane = (int)(t & 63), h = lane >> 5;
+    const size_t ch = t >> 6;
+    const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
+    const uint32_t r = g * 32 + (lane & 31), nsb = k / 256, sb = c / 8, sub = c % 8, j = sub / 2, hb = sub % 2;
+    uint8_t out[16] = {0};
+    float2 side = make_float2(0.0f, 0.0f);
+    if (r < n) {
+        const uint8_t *blk = blocks + ((size_t)r * nsb + sb) * 176, *qh = blk + 16, *qs = blk + 48;
+        // element e of sub-block 2j + hb: nibble hb of qs[32j + e], bit 2j + hb of qh[e]
+        auto val = [&](int e) -> uint8_t {
+            const uint32_t q = (qs[32 * j + e] >> (4 * hb)) & 15u;
+            return (uint8_t)(q | (((uint32_t)(qh[e] >> (2 * j + hb)) & 1u) << 4));
+        };
+        for (int e = 0; e < 8; ++e) {
+            out[e] = val(8 * h + e);
+            out[8 + e] = val(16 + 8 * h + e);
+        }
+        const uint8_t *sc = blk + 4;
+        uint32_t scv, mnv;
+        if (sub < 4) {
+            scv = sc[sub] & 63u;
+            mnv = sc[sub + 4] & 63u;
+        } else {
+            scv = (sc[sub + 4] & 15u) | ((sc[sub - 4] >> 6) << 4);
+            mnv = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4);
+        }
+        const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
+        side = make_float2(d * (float)scv, dmin * (float)mnv);
+    }
+    uint4 v;
+    std::memcpy(&v, out, 16);
+    *(uint4 *)(dq + t * 16) = v;
+    if (lane < 32) dside[ch * 32 + lane] = side;
+}
+
 __global__ void t32_q8_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc, uint8_t *dq,
                                 uint16_t *dside, uint32_t n, uint32_t k, uint32_t G, uint32_t C) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -720,7 +804,7 @@ __global__ void t32_f16_kernel(const uint16_t *__restrict__ src, uint8_t *dq, ui
 uint32_t chunk_k(int type) {
     switch (type) {
     case JANUS_DT_Q4_0: case JANUS_DT_Q4_K: return 64;
-    case JANUS_DT_Q8_0: return 32;
+    case JANUS_DT_Q8_0: case JANUS_DT_Q5_K: return 32;
     default: return 16;
     }
 }
@@ -735,6 +819,7 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
     if (w->type == JANUS_DT_Q4_0) side = (size_t)G * C * 32 * 4;
     else if (w->type == JANUS_DT_Q8_0) side = (size_t)G * C * 32 * 2;
     else if (w->type == JANUS_DT_Q4_K) side = (size_t)G * (C / 4) * 32 * 16;
+    else if (w->type == JANUS_DT_Q5_K) side = (size_t)G * C * 32 * 8;
     void *mem = nullptr;
     JANUS_HIP_CHECK(ctx, hipMalloc(&mem, qbytes + side + 256));
     uint8_t *dq = (uint8_t *)mem, *ds = (uint8_t *)mem + qbytes;
@@ -747,6 +832,9 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
         break;
     case JANUS_DT_Q4_K:
         hipLaunchKernelGGL(t32_q4_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, ds, w->n, w->k, G, C);
+        break;
+    case JANUS_DT_Q5_K:
+        hipLaunchKernelGGL(t32_q5_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, (float2 *)ds, w->n, w->k, G, C);
         break;
     case JANUS_DT_Q8_0:
         hipLaunchKernelGGL(t32_q8_0_kernel, grid, block, 0, ctx->stream, w->qs, w->sc, dq, (uint16_t *)ds, w->n,
@@ -823,7 +911,7 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     a.passes_per_wg = (a.total_passes + ks - 1) / ks;
     a.ksplit = (a.total_passes + a.passes_per_wg - 1) / a.passes_per_wg;
     a.pitch = a.pass_chunks * F::CK + 8;
-    const bool sums = std::is_same<F, GQ4_K>::value;
+    const bool sums = NeedsSums<F>::value;
     size_t lds = (size_t)MT * 32 * a.pitch * 2 + (sums ? (size_t)(kr / 32) * MT * 32 * 4 : 0);
     const size_t red = (size_t)WAVES * KW * 16 * 64 * 4;   // K-slice reduction, one M-tile at a time
     if (lds < red) lds = red;
@@ -878,6 +966,7 @@ int launch_mt(janus_ctx *ctx, const GemmArgs &a, const janus_weight *w, GemmPart
     case JANUS_DT_Q4_0: return launch_mfma<GQ4_0, MT>(ctx, a, w, parts);
     case JANUS_DT_Q8_0: return launch_mfma<GQ8_0, MT>(ctx, a, w, parts);
     case JANUS_DT_Q4_K: return launch_mfma<GQ4_K, MT>(ctx, a, w, parts);
+    case JANUS_DT_Q5_K: return launch_mfma<GQ5_K, MT>(ctx, a, w, parts);
     default: return launch_mfma<GF16, MT>(ctx, a, w, parts);
     }
 }
@@ -1031,7 +1120,7 @@ int run_partials(janus_ctx *ctx, const void *a, const janus_weight *w, uint32_t 
 bool mfma_gemm_supported(int a_dt, const janus_weight *w) {
     if (a_dt != JANUS_DT_F16 || w->k % 8) return false;
     return w->type == JANUS_DT_Q4_0 || w->type == JANUS_DT_Q8_0 || w->type == JANUS_DT_Q4_K ||
-           w->type == JANUS_DT_F16;
+           w->type == JANUS_DT_Q5_K || w->type == JANUS_DT_F16;
 }
 
 int mfma_gemm_prepare(janus_ctx *ctx, const janus_weight *w) {

@@ -13,7 +13,7 @@ from typing import Sequence
 import numpy as np
 
 from . import _lib, gguf, ops
-from ._lib import DT_F16, DT_F32, DT_Q4_0, DT_Q4_K, DT_Q8_0, ModelConfig, check
+from ._lib import DT_F16, DT_F32, DT_Q4_0, DT_Q4_K, DT_Q5_K, DT_Q6_K, DT_Q8_0, ModelConfig, check
 from .ops import ComputeEngine
 from .synth import ModelSpec, Tensor
 
@@ -44,7 +44,7 @@ class Model:
         defaults to its clamped context_length) and every tensor handed to the
         weight upload as the file stores it, read through the memory map.
 
-        A quantised token_embd.weight (Q4_0 / Q8_0 / Q4_K) becomes a binary16
+        A quantised token_embd.weight (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K) becomes a binary16
         table as allocate_tensors does (compute/engine.rs:635-771), but in GGML
         element order for every format: the blocks are dequantised on the GPU by
         the weight upload's closed form and rounded to binary16 (RNE). The
@@ -122,7 +122,7 @@ class Model:
 
 def _gguf_tensor(engine: ComputeEngine, f, t) -> Tensor:
     n, k = t.shape_nk()
-    if t.name == "token_embd.weight" and t.ggml_type in (DT_Q4_0, DT_Q8_0, DT_Q4_K):
+    if t.name == "token_embd.weight" and t.ggml_type in (DT_Q4_0, DT_Q8_0, DT_Q4_K, DT_Q5_K, DT_Q6_K):
         return Tensor(t.name, DT_F16, n, k, _embedding_f16(engine, t.ggml_type, n, k, f.tensor_data(t)))
     return Tensor(t.name, t.ggml_type, n, k, f.tensor_data(t))
 

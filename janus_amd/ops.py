@@ -16,7 +16,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import (DT_F16, DT_F32, DT_Q4_0, DT_Q4_K, DT_Q8_0, TIE_LAST,  # noqa: F401
+from ._lib import (DT_F16, DT_F32, DT_Q4_0, DT_Q4_K, DT_Q5_K, DT_Q6_K, DT_Q8_0, TIE_LAST,  # noqa: F401
                    TIE_WGSL, WEIGHT_FTZ_F16, JanusError, check)
 
 _TORCH_DT = {torch.float32: DT_F32, torch.float16: DT_F16}
@@ -82,7 +82,8 @@ class GpuTensor:
     """GpuTensor (compute/tensor.rs:4-7): an uploaded, library-owned weight.
 
     `data` holds the tensor exactly as a GGUF file stores it (F32/F16 values,
-    or Q4_0/Q8_0/Q4_K blocks) for logical shape [n rows][k cols].
+    or Q4_0/Q8_0/Q4_K/Q5_K/Q6_K blocks) for logical shape [n rows][k cols].
+    A Q6_K upload reports F16 afterwards, as the reference's loader does.
     """
 
     def __init__(self, engine: ComputeEngine, ggml_type: int, n: int, k: int, data, flags: int = 0):
@@ -94,6 +95,10 @@ class GpuTensor:
         engine._check(engine.lib.janus_weight_upload(engine.ctx, ggml_type, n, k, buf.ctypes.data,
                                                      buf.nbytes, flags, C.byref(h)))
         self.handle = h
+        # Q6_K is stored as binary16 after upload (compute/engine.rs:800-831)
+        t = C.c_int()
+        engine._check(engine.lib.janus_weight_info(h, C.byref(t), None, None, None))
+        self.ggml_type = t.value
 
     def dequant(self) -> torch.Tensor:
         out = torch.empty(self.n, self.k, dtype=torch.float32, device=f"cuda:{self.engine.device}")

@@ -11,7 +11,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 QK = 32       # Q4_0 / Q8_0 block width
-QK_K = 256    # Q4_K super-block width
+QK_K = 256    # K-quant super-block width
 
 
 def f16_bits(x: np.ndarray) -> np.ndarray:
@@ -89,6 +89,94 @@ def random_q4_k(rng: np.random.Generator, n: int, k: int, sigma: float = 0.02) -
     return quantize_q4_k(rng.standard_normal((n, k), dtype=np.float32) * np.float32(sigma))
 
 
+def _k_scales(sc: np.ndarray, mq: np.ndarray) -> np.ndarray:
+    """The 12-byte 6-bit scale/min packing shared by block_q4_K and block_q5_K."""
+    scales = np.zeros((sc.shape[0], 12), dtype=np.uint8)
+    scales[:, 0:4] = sc[:, 0:4] & 63
+    scales[:, 4:8] = mq[:, 0:4] & 63
+    scales[:, 8:12] = (sc[:, 4:8] & 15) | ((mq[:, 4:8] & 15) << 4)
+    scales[:, 0:4] |= (sc[:, 4:8] >> 4) << 6
+    scales[:, 4:8] |= (mq[:, 4:8] >> 4) << 6
+    return scales
+
+
+def quantize_q5_k(w: np.ndarray) -> np.ndarray:
+    """Quantise f32 weights [n, k] to GGML block_q5_K bytes {d, dmin, scales[12],
+    qh[32], qs[128]}: the Q4_K scheme with 5-bit values (scale = range / 31);
+    bit 4 of the value for element 64j + 32h + t sits in bit 2j + h of qh[t]."""
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    assert k % QK_K == 0
+    sb = w.reshape(-1, 8, 32)
+    mn = np.minimum(sb.min(axis=2), 0.0)
+    scale = (sb.max(axis=2) - mn) / 31.0
+    moff = -mn
+    d = f16_bits(scale.max(axis=1) / 63.0)
+    dmin = f16_bits(moff.max(axis=1) / 63.0)
+    df = d.view(np.float16).astype(np.float32)
+    dminf = dmin.view(np.float16).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sc = np.where(df[:, None] > 0, np.rint(scale / df[:, None]), 0).clip(0, 63).astype(np.uint8)
+        mq = np.where(dminf[:, None] > 0, np.rint(moff / dminf[:, None]), 0).clip(0, 63).astype(np.uint8)
+        eff_s = df[:, None] * sc.astype(np.float32)
+        eff_m = dminf[:, None] * mq.astype(np.float32)
+        q = np.where(eff_s[:, :, None] > 0, np.rint((sb + eff_m[:, :, None]) / eff_s[:, :, None]), 0)
+    q = q.clip(0, 31).astype(np.uint8).reshape(-1, 4, 2, 32)   # [sb, j, lo/hi, t]
+    nsb = sb.shape[0]
+    qs = ((q[:, :, 0, :] & 15) | ((q[:, :, 1, :] & 15) << 4)).reshape(nsb, 128)
+    qh = np.zeros((nsb, 32), dtype=np.uint8)
+    for j in range(4):
+        qh |= ((q[:, j, 0, :] >> 4) << (2 * j)).astype(np.uint8)
+        qh |= ((q[:, j, 1, :] >> 4) << (2 * j + 1)).astype(np.uint8)
+    out = np.empty((nsb, 176), dtype=np.uint8)
+    out[:, 0:2] = d.view(np.uint8).reshape(nsb, 2)
+    out[:, 2:4] = dmin.view(np.uint8).reshape(nsb, 2)
+    out[:, 4:16] = _k_scales(sc, mq)
+    out[:, 16:48] = qh
+    out[:, 48:] = qs
+    return out.reshape(-1)
+
+
+def random_q5_k(rng: np.random.Generator, n: int, k: int, sigma: float = 0.02) -> np.ndarray:
+    return quantize_q5_k(rng.standard_normal((n, k), dtype=np.float32) * np.float32(sigma))
+
+
+def quantize_q6_k(w: np.ndarray) -> np.ndarray:
+    """Quantise f32 weights [n, k] to GGML block_q6_K bytes {ql[128], qh[64],
+    scales[16] (int8), d}: per 16-element group an int8 scale against d =
+    max(group scale) / 127, values q + 32 in 0..63. Element 128h + 32p + l
+    keeps its low nibble in nibble p // 2 of ql[64h + l + 32 (p % 2)] and its
+    two high bits in bits 2p of qh[32h + l]."""
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    assert k % QK_K == 0
+    g = w.reshape(-1, 16, 16)
+    nsb = g.shape[0]
+    gs = np.abs(g).max(axis=2) / 31.0
+    d = f16_bits(gs.max(axis=1) / 127.0)
+    df = d.view(np.float16).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sc = np.where(df[:, None] > 0, np.rint(gs / df[:, None]), 0).clip(-128, 127).astype(np.int8)
+        eff = df[:, None] * sc.astype(np.float32)
+        q = np.where(eff[:, :, None] != 0, np.rint(g / eff[:, :, None]), 0)
+    q = (q.clip(-32, 31) + 32).astype(np.uint8).reshape(nsb, 2, 4, 32)   # [sb, h, p, l]
+    ql = np.zeros((nsb, 2, 64), dtype=np.uint8)
+    qh = np.zeros((nsb, 2, 32), dtype=np.uint8)
+    for p in range(4):
+        ql[:, :, 32 * (p % 2):32 * (p % 2) + 32] |= ((q[:, :, p, :] & 15) << (4 * (p // 2))).astype(np.uint8)
+        qh |= ((q[:, :, p, :] >> 4) << (2 * p)).astype(np.uint8)
+    out = np.empty((nsb, 210), dtype=np.uint8)
+    out[:, 0:128] = ql.reshape(nsb, 128)
+    out[:, 128:192] = qh.reshape(nsb, 64)
+    out[:, 192:208] = sc.view(np.uint8)
+    out[:, 208:210] = d.view(np.uint8).reshape(nsb, 2)
+    return out.reshape(-1)
+
+
+def random_q6_k(rng: np.random.Generator, n: int, k: int, sigma: float = 0.02) -> np.ndarray:
+    return quantize_q6_k(rng.standard_normal((n, k), dtype=np.float32) * np.float32(sigma))
+
+
 @dataclass
 class Tensor:
     """One GGUF tensor: GGML type id, logical shape (n, k) (k = 0 for 1-D) and bytes."""
@@ -116,7 +204,7 @@ class ModelSpec:
         return self.hidden // self.heads
 
 
-F32, F16, Q4_0, Q8_0, Q4_K = 0, 1, 2, 8, 12
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
 
 
 def _mat(rng, name, qtype, n, k):
@@ -126,6 +214,10 @@ def _mat(rng, name, qtype, n, k):
         return Tensor(name, Q8_0, n, k, random_q8_0(rng, n, k))
     if qtype == Q4_K:
         return Tensor(name, Q4_K, n, k, random_q4_k(rng, n, k))
+    if qtype == Q5_K:
+        return Tensor(name, Q5_K, n, k, random_q5_k(rng, n, k))
+    if qtype == Q6_K:
+        return Tensor(name, Q6_K, n, k, random_q6_k(rng, n, k))
     if qtype == F16:
         return Tensor(name, F16, n, k, f16_bits(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)))
     return Tensor(name, F32, n, k, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))

@@ -161,6 +161,70 @@ void jo_dequant_q4_k(const uint8_t *blocks, size_t nblocks, int ftz, float *out)
     for (size_t b = 0; b < nblocks; ++b) q4k_block(blocks + b * 144, ftz, out + b * 256);
 }
 
+/* Q5_K, GGML dequantize_row_q5_K: the Q4_K header and element order with a
+ * fifth bit per element from qh (bit 2j / 2j+1 of qh[b] for chunk j). */
+static void q5k_block(const uint8_t *blk, int ftz, float *w /*256*/)
+{
+    float d = ftz ? jo_f16_to_f32_ftz(rd16(blk)) : jo_f16_to_f32_exact(rd16(blk));
+    float dmin = ftz ? jo_f16_to_f32_ftz(rd16(blk + 2)) : jo_f16_to_f32_exact(rd16(blk + 2));
+    const uint8_t *scales = blk + 4, *qh = blk + 16, *qs = blk + 48;
+    for (int j = 0; j < 4; ++j) {
+        uint8_t sl, ml, sh, mh;
+        jo_q4_k_scale_min(scales, 2 * j, &sl, &ml);
+        jo_q4_k_scale_min(scales, 2 * j + 1, &sh, &mh);
+        float scale_lo = d * (float)sl, min_lo = dmin * (float)ml;
+        float scale_hi = d * (float)sh, min_hi = dmin * (float)mh;
+        for (int b = 0; b < 32; ++b) {
+            uint8_t byte = qs[32 * j + b];
+            unsigned lo = (byte & 15u) | (((qh[b] >> (2 * j)) & 1u) << 4);
+            unsigned hi = (byte >> 4) | (((qh[b] >> (2 * j + 1)) & 1u) << 4);
+            w[64 * j + b] = scale_lo * (float)lo - min_lo;
+            w[64 * j + 32 + b] = scale_hi * (float)hi - min_hi;
+        }
+    }
+}
+
+void jo_dequant_q5_k(const uint8_t *blocks, size_t nblocks, int ftz, float *out)
+{
+    for (size_t b = 0; b < nblocks; ++b) q5k_block(blocks + b * 176, ftz, out + b * 256);
+}
+
+void jo_dequant_q6_k(const uint8_t *blocks, size_t nblocks, int ref_order, float *out)
+{
+    for (size_t bi = 0; bi < nblocks; ++bi) {
+        const uint8_t *blk = blocks + bi * 210;
+        const uint8_t *ql = blk, *qh = blk + 128;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        float d = jo_f16_to_f32_exact(rd16(blk + 208));
+        float *w = out + bi * 256;
+        if (ref_order) {
+            /* compute/engine.rs:221-241 */
+            for (int i = 0; i < 256; ++i) {
+                unsigned lo = (i % 2 == 0) ? (ql[i / 2] & 15u) : (ql[i / 2] >> 4);
+                unsigned hi = (qh[i / 4] >> (2 * (i % 4))) & 3u;
+                int q = (int)((hi << 4) | lo) - 32;
+                w[i] = d * (float)sc[i / 16] * (float)q;
+            }
+            continue;
+        }
+        for (int h = 0; h < 2; ++h) {
+            const uint8_t *l8 = ql + 64 * h, *h8 = qh + 32 * h;
+            const int8_t *s8 = sc + 8 * h;
+            for (int l = 0; l < 32; ++l) {
+                int is = l / 16;
+                int q1 = (int)((l8[l] & 15u) | ((h8[l] & 3u) << 4)) - 32;
+                int q2 = (int)((l8[l + 32] & 15u) | (((h8[l] >> 2) & 3u) << 4)) - 32;
+                int q3 = (int)((l8[l] >> 4) | (((h8[l] >> 4) & 3u) << 4)) - 32;
+                int q4 = (int)((l8[l + 32] >> 4) | (((h8[l] >> 6) & 3u) << 4)) - 32;
+                w[128 * h + l] = d * (float)s8[is] * (float)q1;
+                w[128 * h + l + 32] = d * (float)s8[is + 2] * (float)q2;
+                w[128 * h + l + 64] = d * (float)s8[is + 4] * (float)q3;
+                w[128 * h + l + 96] = d * (float)s8[is + 6] * (float)q4;
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* matrix-vector products                                                   */
 /* ------------------------------------------------------------------------ */
@@ -224,6 +288,27 @@ int jo_num_threads(void)
 #else
     return 1;
 #endif
+}
+
+void jo_gemv_q5_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k, int ftz)
+{
+    uint32_t nb = k / 256;
+    float wv[256];
+    for (uint32_t r = 0; r < n; ++r) {
+        float row = 0.0f;
+        for (uint32_t b = 0; b < nb; ++b) {
+            q5k_block(w + ((size_t)r * nb + b) * 176, ftz, wv);
+            const float *xv = x + (size_t)b * 256;
+            float s = 0.0f;
+            for (int j = 0; j < 4; ++j)
+                for (int bi = 0; bi < 32; ++bi) {
+                    s = s + wv[64 * j + bi] * xv[64 * j + bi];
+                    s = s + wv[64 * j + 32 + bi] * xv[64 * j + 32 + bi];
+                }
+            row += s;
+        }
+        y[r] = row;
+    }
 }
 
 void jo_gemv_q4_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k, int ftz)

@@ -52,6 +52,32 @@ void jo_dequant_q4_0(const uint8_t *blocks, size_t nblocks, float *out);
 void jo_dequant_q4_k(const uint8_t *blocks, size_t nblocks, int ftz, float *out);
 /* get_scale_min_k4 restated from extract_6bit_from_packed, gemm_q4_k.wgsl:120-147 */
 void jo_q4_k_scale_min(const uint8_t *scales12, int j, uint8_t *sc, uint8_t *mn);
+/* Q5_K: 176-byte GGML block_q5_K {f16 d, dmin; u8 scales[12]; u8 qh[32];
+ * u8 qs[128]} in GGML element order (ggml-quants.c dequantize_row_q5_K, the
+ * published llama.cpp layout; the reference's shaders/gemm_q5_k.wgsl:6-23
+ * reads these bytes at other offsets, so GGML defines it here): for chunk
+ * j = 0..3, b = 0..31, with (sc, m) from jo_q4_k_scale_min:
+ *   w[64j+b]    = (d*sc[2j])   * (qs[32j+b] & 15 | bit 2j   of qh[b] << 4) - dmin*m[2j]
+ *   w[64j+32+b] = (d*sc[2j+1]) * (qs[32j+b] >> 4 | bit 2j+1 of qh[b] << 4) - dmin*m[2j+1]
+ * rounded as the Q4_K form (product, then difference); ftz as for Q4_K. */
+void jo_dequant_q5_k(const uint8_t *blocks, size_t nblocks, int ftz, float *out);
+/* Q5_K product, the Q4_K accumulation order (per 64-chunk, per byte: low
+ * then high element). */
+void jo_gemv_q5_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k, int ftz);
+/* Q6_K: 210-byte block {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}.
+ * ref_order == 0: GGML element order (ggml-quants.c dequantize_row_q6_K): half
+ * h = 0,1 uses ql[64h..], qh[32h..], scales[8h..]; for l = 0..31, is = l/16:
+ *   w[128h+l]    = (d*sc[is])   * ((ql[l]    & 15 | (qh[l]     & 3) << 4) - 32)
+ *   w[128h+l+32] = (d*sc[is+2]) * ((ql[l+32] & 15 | (qh[l]>>2 & 3) << 4) - 32)
+ *   w[128h+l+64] = (d*sc[is+4]) * ((ql[l]    >> 4 | (qh[l]>>4 & 3) << 4) - 32)
+ *   w[128h+l+96] = (d*sc[is+6]) * ((ql[l+32] >> 4 | (qh[l]>>6 & 3) << 4) - 32)
+ * ref_order != 0: the reference's own loader order, compute/engine.rs:198-248:
+ * element i takes nibble i%2 of ql[i/2], bits 2(i%4) of qh[i/4], scale
+ * scales[i/16]: w = (d*s)*(q-32). d decoded exactly (engine.rs:221).
+ * Pinned by special values, single-bit brute force and a hand-worked
+ * reference-order known answer; GGML element placement beyond the spot
+ * checks of element l and l+96: parity unpinned (no GGML build here). */
+void jo_dequant_q6_k(const uint8_t *blocks, size_t nblocks, int ref_order, float *out);
 
 /* ---- matrix-vector products in the reference's accumulation order ------ */
 /* gemm_q8_0.wgsl:74-128: per element sum += (d*q)*x; per block row += sum. */

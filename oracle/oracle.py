@@ -42,6 +42,9 @@ _SIG = {
     "jo_dequant_q4_0": (None, [_u8p, SZ, _f32p]),
     "jo_dequant_q4_k": (None, [_u8p, SZ, I32, _f32p]),
     "jo_q4_k_scale_min": (None, [_u8p, I32, C.POINTER(C.c_uint8), C.POINTER(C.c_uint8)]),
+    "jo_dequant_q5_k": (None, [_u8p, SZ, I32, _f32p]),
+    "jo_gemv_q5_k": (None, [_u8p, _f32p, _f32p, U32, U32, I32]),
+    "jo_dequant_q6_k": (None, [_u8p, SZ, I32, _f32p]),
     "jo_gemv_q8_0": (None, [_u8p, _f32p, _f32p, U32, U32]),
     "jo_gemv_q4_k": (None, [_u8p, _f32p, _f32p, U32, U32, I32]),
     "jo_gemv_q4_0": (None, [_u8p, _f32p, _f32p, U32, U32]),
@@ -102,8 +105,11 @@ def f16_to_f32(bits, mode: str = "exact") -> np.ndarray:
 
 # ---- dequantisation and products ------------------------------------------------
 
-def dequant(ggml_type: int, data: np.ndarray, n: int, k: int, ftz: bool = False) -> np.ndarray:
-    """Reference dequantisation of GGUF bytes (or F32/F16 values) to f32 [n, k]."""
+def dequant(ggml_type: int, data: np.ndarray, n: int, k: int, ftz: bool = False,
+            q6k_ref_order: bool = False) -> np.ndarray:
+    """Reference dequantisation of GGUF bytes (or F32/F16 values) to f32 [n, k].
+    Q6_K uses GGML's element order unless q6k_ref_order selects the
+    reference loader's (compute/engine.rs:198-248)."""
     L = lib()
     out = np.empty(n * k, dtype=np.float32)
     if ggml_type == 8:
@@ -112,6 +118,10 @@ def dequant(ggml_type: int, data: np.ndarray, n: int, k: int, ftz: bool = False)
         L.jo_dequant_q4_0(np.ascontiguousarray(data, dtype=np.uint8), n * k // 32, out)
     elif ggml_type == 12:
         L.jo_dequant_q4_k(np.ascontiguousarray(data, dtype=np.uint8), n * k // 256, int(ftz), out)
+    elif ggml_type == 13:
+        L.jo_dequant_q5_k(np.ascontiguousarray(data, dtype=np.uint8), n * k // 256, int(ftz), out)
+    elif ggml_type == 14:
+        L.jo_dequant_q6_k(np.ascontiguousarray(data, dtype=np.uint8), n * k // 256, int(q6k_ref_order), out)
     elif ggml_type == 1:
         out = f16_to_f32(np.asarray(data).view(np.uint16), "ftz" if ftz else "exact")
     elif ggml_type == 0:
@@ -138,6 +148,12 @@ def gemm_auto(x: np.ndarray, ggml_type: int, data: np.ndarray, n: int, k: int) -
         L.jo_gemv_q8_0(np.ascontiguousarray(data, dtype=np.uint8), x, y, n, k)
     elif ggml_type == 12:
         L.jo_gemv_q4_k(np.ascontiguousarray(data, dtype=np.uint8), x, y, n, k, 1)
+    elif ggml_type == 13:
+        L.jo_gemv_q5_k(np.ascontiguousarray(data, dtype=np.uint8), x, y, n, k, 0)
+    elif ggml_type == 14:
+        # the reference loads Q6_K as binary16 weights (engine.rs:800-831)
+        bits = f32_to_f16_rne(dequant(14, data, n, k))
+        L.jo_gemm_f16(x, bits, y, 1, 1, k, n)
     elif ggml_type == 2:
         L.jo_gemv_q4_0(np.ascontiguousarray(data, dtype=np.uint8), x, y, n, k)
     elif ggml_type in (0, 1):

@@ -65,10 +65,16 @@ def test_weight_upload_validation(vctx):
     assert _upload(lib, ctx, _lib.DT_Q4_K, 4, 128, np.zeros(4 * 72, np.uint8)) == _lib.E_INVALID_DIM
     # byte size mismatch
     assert _upload(lib, ctx, _lib.DT_Q4_0, 4, 64, np.zeros(10, np.uint8)) == _lib.E_INVALID_DIM
-    # unsupported GGML type (Q5_K = 13, Q6_K = 14) -> error instead of panic (quantized.rs:181)
-    assert _upload(lib, ctx, 14, 4, 256, np.zeros(4 * 210, np.uint8)) == _lib.E_UNSUPPORTED_DTYPE
+    assert _upload(lib, ctx, _lib.DT_Q5_K, 4, 128, np.zeros(4 * 88, np.uint8)) == _lib.E_INVALID_DIM
+    assert _upload(lib, ctx, _lib.DT_Q5_K, 4, 256, np.zeros(4 * 176 - 1, np.uint8)) == _lib.E_INVALID_DIM
+    assert _upload(lib, ctx, _lib.DT_Q6_K, 4, 256, np.zeros(4 * 210 + 2, np.uint8)) == _lib.E_INVALID_DIM
+    assert b"blocks of 210" in lib.janus_last_error(ctx)
+    # unsupported GGML type (Q2_K = 10) -> error instead of panic (quantized.rs:181)
+    assert _upload(lib, ctx, 10, 4, 256, np.zeros(4 * 84, np.uint8)) == _lib.E_UNSUPPORTED_DTYPE
     # a valid tensor passes every host check and then needs the device
     assert _upload(lib, ctx, _lib.DT_Q8_0, 4, 64, raw) == _lib.E_NO_DEVICE
+    assert _upload(lib, ctx, _lib.DT_Q5_K, 4, 256, np.zeros(4 * 176, np.uint8)) == _lib.E_NO_DEVICE
+    assert _upload(lib, ctx, _lib.DT_Q6_K, 4, 256, np.zeros(4 * 210, np.uint8)) == _lib.E_NO_DEVICE
 
 
 def test_op_validation(vctx):

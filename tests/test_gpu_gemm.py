@@ -18,7 +18,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-GEN = {2: synth.random_q4_0, 8: synth.random_q8_0, 12: synth.random_q4_k}
+GEN = {2: synth.random_q4_0, 8: synth.random_q8_0, 12: synth.random_q4_k, 13: synth.random_q5_k}
 
 
 def _weight(engine, ggml_type, n, k, seed):
@@ -44,7 +44,7 @@ def _check_against_f64(y, wf, a16):
     assert np.all(err <= bound), float(np.max(err / bound))
 
 
-@pytest.mark.parametrize("ggml_type", [2, 8, 12, 1])
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
 @pytest.mark.parametrize("rows", [2, 7, 32, 33, 64])
 @pytest.mark.parametrize("n,k", [(96, 256), (200, 512), (4096, 4096), (1024, 14336)])
 def test_mfma_gemm_matches_stacked_gemv_and_f64(engine, ggml_type, rows, n, k):
@@ -65,7 +65,7 @@ def test_mfma_gemm_matches_stacked_gemv_and_f64(engine, ggml_type, rows, n, k):
     _check_against_f64(stacked.cpu().numpy(), wf, a16)
 
 
-@pytest.mark.parametrize("ggml_type", [2, 8, 12])
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 13])
 @pytest.mark.parametrize("rows", [32, 48, 64])
 @pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336)])
 def test_pipelined_gemm_shapes_match_f64(engine, ggml_type, rows, n, k):

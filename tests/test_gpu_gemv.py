@@ -18,7 +18,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-GEN = {2: synth.random_q4_0, 8: synth.random_q8_0, 12: synth.random_q4_k}
+GEN = {2: synth.random_q4_0, 8: synth.random_q8_0, 12: synth.random_q4_k, 13: synth.random_q5_k}
 
 
 def _weight(engine, ggml_type, n, k, seed, flags=0):
@@ -36,7 +36,7 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).reshape(-1).view(np.uint32)
 
 
-@pytest.mark.parametrize("ggml_type,flags", [(2, 0), (8, 0), (12, 0), (12, 1), (1, 0), (1, 1), (0, 1)])
+@pytest.mark.parametrize("ggml_type,flags", [(2, 0), (8, 0), (12, 0), (12, 1), (13, 0), (13, 1), (1, 0), (1, 1), (0, 1)])
 def test_dequant_bit_exact(engine, ggml_type, flags):
     n, k = 24, 512
     raw, w = _weight(engine, ggml_type, n, k, 10 + ggml_type, flags)
@@ -45,8 +45,8 @@ def test_dequant_bit_exact(engine, ggml_type, flags):
         r = raw.reshape(-1, bb)
         r[:5, :2] = np.array([0x0001, 0x03FF, 0x7C00, 0xFC00, 0x7E01], np.uint16).view(np.uint8).reshape(-1, 2)
         w = ops.GpuTensor(engine, ggml_type, n, k, raw, flags)
-    if ggml_type == 12:
-        r = raw.reshape(-1, 144)
+    if ggml_type in (12, 13):
+        r = raw.reshape(-1, 144 if ggml_type == 12 else 176)
         r[0, 0:2] = np.array([0x0005], np.uint16).view(np.uint8)
         w = ops.GpuTensor(engine, ggml_type, n, k, raw, flags)
     got = w.dequant().cpu().numpy()
@@ -60,10 +60,10 @@ def _bound(wf, x):
 
 
 # the reference decodes F16 weights and Q4_K d/dmin with f16_to_f32_safe
-FTZ = {0: 1, 1: 1, 2: 0, 8: 0, 12: 1}
+FTZ = {0: 1, 1: 1, 2: 0, 8: 0, 12: 1, 13: 0}
 
 
-@pytest.mark.parametrize("ggml_type", [2, 8, 12, 1])
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
 @pytest.mark.parametrize("n,k", [(1, 256), (7, 256), (64, 256), (130, 512), (256, 4096), (96, 14336)])
 def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
     raw, w = _weight(engine, ggml_type, n, k, n + k, FTZ[ggml_type])
@@ -80,8 +80,8 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
     assert np.all(np.abs(got - want) <= 2 * b)
 
 
-@pytest.mark.parametrize("ggml_type", [2, 8, 12, 1])
-@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096)])
+@pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
+@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
     raw, w = _weight(engine, ggml_type, n, k, 3 * n + k, FTZ[ggml_type])
     rng = np.random.default_rng(n)

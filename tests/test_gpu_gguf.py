@@ -29,7 +29,8 @@ def test_gguf_config1_greedy_matches_golden(engine, tmp_path, alignment):
     m.close()
 
 
-@pytest.mark.parametrize("qtype,gen", [(8, synth.random_q8_0), (2, synth.random_q4_0), (12, synth.random_q4_k)])
+@pytest.mark.parametrize("qtype,gen", [(8, synth.random_q8_0), (2, synth.random_q4_0), (12, synth.random_q4_k),
+                                       (13, synth.random_q5_k), (14, synth.random_q6_k)])
 def test_gguf_quantised_embedding_is_the_f16_rounded_dequant(engine, tmp_path, qtype, gen):
     """A quantised token_embd.weight is loaded as the binary16 rounding of its
     GGML-order dequantisation: the model built from the file and one built
