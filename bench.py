@@ -173,15 +173,29 @@ def decode_bs32(engine, spec, steps: int, warmup: int):
     return ms, int(lens.sum())
 
 
-def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
-    """HIP-event timing of back-to-back Q4_0 GEMV launches captured in a graph."""
+def _weight_bytes(rng, qtype: int, n: int, k: int) -> np.ndarray:
+    """GGUF bytes of an [n][k] weight. K-quants quantise 512 N(0, 0.02) rows and
+    repeat them (quantising 58 M weights in numpy takes seconds; the bytes
+    streamed per launch are the same)."""
+    from janus_amd import synth
+    if qtype == 2:
+        return synth.random_q4_0(rng, n, k)
+    rows = min(n, 512)
+    gen = {12: synth.random_q4_k, 13: synth.random_q5_k}[qtype]
+    base = gen(rng, rows, k).reshape(rows, -1)
+    return np.ascontiguousarray(np.tile(base, ((n + rows - 1) // rows, 1))[:n]).reshape(-1)
+
+
+def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200, qtype: int = 2):
+    """HIP-event timing of back-to-back GEMV launches (Q4_0 unless qtype says
+    otherwise) captured in a graph."""
     import torch
-    from janus_amd import ops, synth
+    from janus_amd import ops
     rng = np.random.default_rng(2)
-    raw = synth.random_q4_0(rng, n, k)
+    raw = _weight_bytes(rng, qtype, n, k)
     nbytes = raw.nbytes
     copies = max(2, int(np.ceil(400e6 / nbytes)))
-    ws = [ops.GpuTensor(engine, ops.DT_Q4_0, n, k, raw) for _ in range(copies)]
+    ws = [ops.GpuTensor(engine, qtype, n, k, raw) for _ in range(copies)]
     x = torch.from_numpy(rng.standard_normal(k).astype(np.float16)).cuda()
     y = torch.empty(n, dtype=torch.float16, device="cuda")
     for i in range(copies):
@@ -211,17 +225,17 @@ def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200):
     return us, algo, copies
 
 
-def gemm_m32(engine, n: int, k: int, rows: int = 32, launches: int = 100):
+def gemm_m32(engine, n: int, k: int, rows: int = 32, launches: int = 100, qtype: int = 2):
     """The small-M product of config 5 at one layer shape: 32 binary16 rows x a
-    Q4_0 weight (MFMA GEMM + split-K reduce, fp16 output) through
-    janus_gemm_auto, graph-replayed over > 400 MB of weight copies. Returns
-    (us per launch, algorithmic bytes, flops)."""
+    quantised weight (Q4_0 unless qtype says otherwise; MFMA GEMM + split-K
+    reduce, fp16 output) through janus_gemm_auto, graph-replayed over > 400 MB
+    of weight copies. Returns (us per launch, algorithmic bytes, flops)."""
     import torch
-    from janus_amd import ops, synth
+    from janus_amd import ops
     rng = np.random.default_rng(12)
-    raw = synth.random_q4_0(rng, n, k)
+    raw = _weight_bytes(rng, qtype, n, k)
     copies = max(2, int(np.ceil(400e6 / raw.nbytes)))
-    ws = [ops.GpuTensor(engine, ops.DT_Q4_0, n, k, raw) for _ in range(copies)]
+    ws = [ops.GpuTensor(engine, qtype, n, k, raw) for _ in range(copies)]
     a = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float16)).cuda()
     y = torch.empty(rows, n, dtype=torch.float16, device="cuda")
     for i in range(copies):
@@ -329,7 +343,8 @@ def main() -> int:
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3", "gemm"], default="all",
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3", "gemm", "kquant"],
+                    default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -364,6 +379,24 @@ def main() -> int:
             log(f"  Q4_0 GEMM M=32 {n}x{k}: {u:.2f} us, {b / u / 1e3:.0f} GB/s, {fl / u / 1e6:.0f} TFLOP/s "
                 f"({fl / u / 1e6 / MFMA_PEAK_TFLOPS:.3f} of dense fp16 MFMA)")
         if args.only == "gemm":
+            return 0
+    kq = None
+    if args.only in ("all", "kquant"):
+        # K-quant products at the Llama-3-8B decode shapes (x fp16, y fp16)
+        kq = {}
+        for qname, qt in (("q4_k", 12), ("q5_k", 13)):
+            for n, k in ((14336, 4096), (4096, 14336)):
+                u, b, _ = gemv_roofline(engine, n, k, qtype=qt)
+                kq[f"gemv_{qname}_{n}x{k}"] = {"us_per_launch": round(u, 3), "GB_s": round(b / u / 1e3, 1),
+                                               "frac": round(b / u / 1e3 / HBM_PEAK_GBS, 4)}
+                log(f"  {qname.upper()} GEMV {n}x{k}: {u:.2f} us/launch, {b / u / 1e3:.0f} GB/s "
+                    f"({b / u / 1e3 / HBM_PEAK_GBS:.3f} of 8 TB/s)")
+        u, b, fl = gemm_m32(engine, 14336, 4096, qtype=13)
+        kq["gemm_m32_q5_k_14336x4096"] = {"us_per_launch": round(u, 2), "GB_s": round(b / u / 1e3, 1),
+                                          "TFLOP_s": round(fl / u / 1e6, 1),
+                                          "mfma_frac": round(fl / u / 1e6 / MFMA_PEAK_TFLOPS, 4)}
+        log(f"  Q5_K GEMM M=32 14336x4096: {u:.2f} us, {b / u / 1e3:.0f} GB/s, {fl / u / 1e6:.0f} TFLOP/s")
+        if args.only == "kquant":
             return 0
     if args.only in ("all", "roofline"):
         log("roofline: Q4_0 GEMV 14336x4096")
@@ -442,6 +475,7 @@ def main() -> int:
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
         "gemm_m32_q4_0": gemm,
+        "kquant": kq,
         "llama2_7b_q4k_c3": c3,
         "attention_c4": attn,
         "cpu_baseline": cpu,

@@ -29,9 +29,6 @@
 
 namespace {
 
-#ifndef JANUS_GEMV_WPC
-#define JANUS_GEMV_WPC 16    // most resident wavefronts per CU the register kernel's grid asks for
-#endif
 #ifndef JANUS_GEMV_NT
 #define JANUS_GEMV_NT 1      // stream weights with non-temporal loads
 #endif
@@ -437,39 +434,41 @@ struct FQ4_K {
     }
 };
 
-// ---- Q5_K: GGML 176-byte super-blocks {d, dmin, scales[12], qh[32], qs[128]} --
+// ---- Q5_K: GGML 176-byte super-blocks {d, dmin, scales[12], qh, qs[128]} ----
 // Same header, sub-block scales and element order as Q4_K (a unit is one
-// 16-byte chunk of qs, x layout shared), plus a fifth bit per element: chunk
-// c = 2j + h covers qh bytes 16h..16h+15, bit 2j for the low nibbles and bit
-// 2j + 1 for the high ones (ggml-quants.c dequantize_row_q5_K). Weight =
-// (d*sc)*q - dmin*m with q in 0..31.
+// 16-byte chunk of qs, x layout shared), plus a fifth bit per element
+// (ggml-quants.c dequantize_row_q5_K). The upload rewrites qh as one word per
+// chunk (bytes 16 + 4c), bit 8 (t % 4) + t / 4 (+ 4 for the high nibble) for
+// quant byte t, so (w >> i) & 0x01010101 sits under the bytes of quant word
+// i. Weight = (d*sc)*q - dmin*m with q in 0..31.
 struct FQ5_K : FQ4_K {
-    struct W { uint4 q; uint4 qh; uint32_t hw; };
+    struct W { uint4 q; uint32_t qh; uint32_t hw; };
     __device__ static W load(WPtr w, size_t unit) {
         size_t sb = unit >> 3;
         int c = (int)(unit & 7);
         const uint4 *blk = (const uint4 *)(w.qs + sb * 176);
         W r;
         r.hw = ((const uint32_t *)blk)[__lane_id() & 3];
-        r.qh = ld_stream(blk + 1 + (c & 1));
+#if !defined(JANUS_GEMV_NT) || JANUS_GEMV_NT
+        r.qh = __builtin_nontemporal_load((const uint32_t *)blk + 4 + c);
+#else
+        r.qh = ((const uint32_t *)blk)[4 + c];
+#endif
         r.q = ld_stream(blk + 3 + c);
         return r;
     }
-    // 5-bit values of the four bytes of q word i: low (lo) and high (hi) elements
-    __device__ static void q5(const W &w, int i, int j, uint32_t &lo, uint32_t &hi) {
+    // 5-bit values of the four bytes of quant word i: low (lo) and high (hi) elements
+    __device__ static void q5(const W &w, int i, uint32_t &lo, uint32_t &hi) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-        const uint32_t h[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
-        const uint32_t hb = h[i] >> (2 * j);
-        lo = (q[i] & 0x0f0f0f0fu) | ((hb & 0x01010101u) << 4);
-        hi = ((q[i] >> 4) & 0x0f0f0f0fu) | ((hb & 0x02020202u) << 3);
+        lo = (q[i] & 0x0f0f0f0fu) | (((w.qh >> i) & 0x01010101u) << 4);
+        hi = ((q[i] >> 4) & 0x0f0f0f0fu) | (((w.qh >> (4 + i)) & 0x01010101u) << 4);
     }
     __device__ static float dot(const W &w, const XF &x) {
-        const int j = x.c >> 1;
         float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint32_t lo, hi;
-            q5(w, i, j, lo, hi);
+            q5(w, i, lo, hi);
             l0 = fmaf(cvt_b0(lo), x.lo[i].x, l0);
             l1 = fmaf(cvt_b1(lo), x.lo[i].y, l1);
             l0 = fmaf(cvt_b2(lo), x.lo[i].z, l0);
@@ -482,14 +481,13 @@ struct FQ5_K : FQ4_K {
         return finish(w, x, l0 + l1, h0 + h1);
     }
     __device__ static float dot(const W &w, const XH &x) {
-        const int j = x.c >> 1;
         const jh2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
         const uint32_t m = vgpr_const_6400();
         float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint32_t lo, hi;
-            q5(w, i, j, lo, hi);
+            q5(w, i, lo, hi);
             // bytes 0, 2 and 1, 3 of each word as binary16 1024 + q (q <= 31 is exact)
             jh2 a = as_h2((lo & 0x001f001fu) | m) - off;
             jh2 c = as_h2(((lo >> 8) & 0x001f001fu) | m) - off;
@@ -1106,19 +1104,20 @@ int launch_fmt(janus_ctx *ctx, const GemvArgs &a) {
 }
 
 // Persistent grid: as many workgroups as can be resident at once (from the
-// occupancy the compiled kernel allows, capped at JANUS_GEMV_WPC wavefronts
+// occupancy the compiled kernel allows, capped at ctx->gemv_wpc wavefronts
 // per CU); each wavefront then walks several row groups.
 template <class F, typename XT, int BPL, int R>
 int launch_reg(janus_ctx *ctx, const GemvArgs &a) {
-    static int per_cu = 0;
-    if (per_cu == 0) {
+    static int occ = 0;
+    if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_reg_kernel<F, XT, BPL, R>, 256, 0) != hipSuccess ||
             nb < 1)
             nb = 1;
-        per_cu = nb < JANUS_GEMV_WPC / 4 ? nb : JANUS_GEMV_WPC / 4;
-        if (per_cu < 1) per_cu = 1;
+        occ = nb;
     }
+    int per_cu = occ < (int)ctx->gemv_wpc / 4 ? occ : (int)ctx->gemv_wpc / 4;
+    if (per_cu < 1) per_cu = 1;
     const uint32_t groups = (a.n + R - 1) / R;
     uint32_t blocks = (groups + 3) / 4;
     const uint32_t cap = (uint32_t)ctx->num_cus * per_cu;
@@ -1162,12 +1161,15 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     const uint32_t nblk = (a.k + XB - 1) / XB;
     const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
-    int &pc = per_cu[norm ? 1 : 0];
-    if (pc == 0) {
+    int &occ = per_cu[norm ? 1 : 0];
+    if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 512, 40 * 1024) != hipSuccess || nb < 1) nb = 1;
-        pc = nb > 2 ? 2 : nb;
+        occ = nb;
     }
+    const int wg_cap = (int)ctx->gemv_lds_wpc / 8;   // 8 wavefronts per workgroup
+    int pc = occ < wg_cap ? occ : wg_cap;
+    if (pc < 1) pc = 1;
     const uint32_t groups = (a.n + R - 1) / R;
     uint32_t blocks = (groups + 7) / 8;
     const uint32_t cap = (uint32_t)ctx->num_cus * pc;

@@ -23,6 +23,11 @@ struct janus_ctx {
     // binary16 M = 1 products with long rows use the LDS-staged kernel
     // (JANUS_GEMV_KERNEL=reg selects the register-resident one instead).
     bool gemv_lds = true;
+    // M = 1 products: most resident wavefronts per CU the grids ask for, for
+    // the register kernel and the LDS-staged kernel (JANUS_GEMV_WPC,
+    // JANUS_GEMV_LDS_WPC)
+    uint32_t gemv_wpc = 16;
+    uint32_t gemv_lds_wpc = 16;
     // binary16-cache attention scores on MFMA (JANUS_ATTN_KERNEL=valu selects
     // the all-VALU kernel instead, for comparisons).
     bool attn_valu = false;
@@ -46,6 +51,8 @@ struct janus_ctx {
 //         sc  = n * nb binary16 scales (nb = k / 32)
 //  Q8_0 : qs  = n * nb * 32 bytes (int8), sc = n * nb binary16 scales
 //  Q4_K : qs  = the GGML 144-byte super-blocks, unchanged, 256-B aligned base
+//  Q5_K : qs  = the GGML 176-byte super-blocks with qh[32] rewritten as one
+//         32-bit word of high bits per 16-byte quant chunk (q5k_pack_high_bits)
 //  F16  : qs  = n * k binary16, row-major, FTZ applied at upload when flagged
 struct janus_weight {
     int type = 0;

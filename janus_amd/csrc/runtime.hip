@@ -121,6 +121,29 @@ inline uint16_t f32_to_f16_host(float f) {
 
 inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+// Q5_K in HBM: the GGML block with its 32 qh bytes rewritten as one 32-bit
+// word per 16-byte quant chunk c = 2j + h (bytes 16 + 4c): for t = 0..15,
+// bit 8 (t % 4) + t / 4 is the fifth bit of the low-nibble element of qs
+// byte 32j + 16h + t (bit 2j of qh[16h + t]) and bit 8 (t % 4) + 4 + t / 4
+// that of its high-nibble element (bit 2j + 1). A kernel then holds one
+// register of high bits per chunk, and (w >> i) & 0x01010101 puts the bits
+// of quant word i under its four bytes.
+void q5k_pack_high_bits(uint8_t *blk) {
+    uint8_t qh[32];
+    std::memcpy(qh, blk + 16, 32);
+    for (int c = 0; c < 8; ++c) {
+        const int j = c / 2, h = c % 2;
+        uint32_t w = 0;
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t b = qh[16 * h + t];
+            const int pos = 8 * (t % 4) + t / 4;
+            w |= ((b >> (2 * j)) & 1u) << pos;
+            w |= ((b >> (2 * j + 1)) & 1u) << (pos + 4);
+        }
+        for (int i = 0; i < 4; ++i) blk[16 + 4 * c + i] = (uint8_t)(w >> (8 * i));
+    }
+}
+
 // ---- dequantisation kernels (debug/bit-exactness entry) --------------------
 
 __global__ void dequant_q4_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc,
@@ -175,9 +198,9 @@ __global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ blocks, float *_
     }
 }
 
-// Q5_K (GGML block_q5_K): the Q4_K form with a fifth bit per element, bit 2j
-// (low nibbles) or 2j + 1 (high nibbles) of qh[t]. (d*sc)*q is exact in
-// binary32 (11 + 6 + 5 bits), so the one rounding is the difference.
+// Q5_K (GGML block_q5_K, high bits packed per chunk by q5k_pack_high_bits):
+// the Q4_K form with a fifth bit per element. (d*sc)*q is exact in binary32
+// (11 + 6 + 5 bits), so the one rounding is the difference.
 __global__ void dequant_q5_k_kernel(const uint8_t *__restrict__ blocks, float *__restrict__ out,
                                     size_t nblocks) {
     size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -185,7 +208,8 @@ __global__ void dequant_q5_k_kernel(const uint8_t *__restrict__ blocks, float *_
     const uint8_t *blk = blocks + b * 176;
     float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
     float dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
-    const uint8_t *qh = blk + 16, *qs = blk + 48;
+    const uint32_t *qh = (const uint32_t *)(blk + 16);
+    const uint8_t *qs = blk + 48;
     for (int j = 0; j < 4; ++j) {
         int sl, ml, sh, mh;
         q4k_scale_min(blk + 4, 2 * j, sl, ml);
@@ -194,8 +218,10 @@ __global__ void dequant_q5_k_kernel(const uint8_t *__restrict__ blocks, float *_
         float scale_hi = d * (float)sh, min_hi = dmin * (float)mh;
         for (int t = 0; t < 32; ++t) {
             const uint8_t byte = qs[32 * j + t];
-            const int lo = (byte & 15) | (((qh[t] >> (2 * j)) & 1) << 4);
-            const int hi = (byte >> 4) | (((qh[t] >> (2 * j + 1)) & 1) << 4);
+            const uint32_t w = qh[2 * j + t / 16];
+            const int pos = 8 * (t % 4) + (t % 16) / 4;
+            const int lo = (byte & 15) | (int)(((w >> pos) & 1u) << 4);
+            const int hi = (byte >> 4) | (int)(((w >> (pos + 4)) & 1u) << 4);
             out[b * 256 + 64 * j + t] = scale_lo * (float)lo - min_lo;
             out[b * 256 + 64 * j + 32 + t] = scale_hi * (float)hi - min_hi;
         }
@@ -268,6 +294,14 @@ int janus_create(int hip_device, janus_ctx **out) {
     if (const char *k = std::getenv("JANUS_ATTN_WPC")) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 1 && v <= 32) ctx->attn_wpc = (uint32_t)v;
+    }
+    if (const char *k = std::getenv("JANUS_GEMV_WPC")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v >= 4 && v <= 64) ctx->gemv_wpc = (uint32_t)v;
+    }
+    if (const char *k = std::getenv("JANUS_GEMV_LDS_WPC")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v >= 8 && v <= 64) ctx->gemv_lds_wpc = (uint32_t)v;
     }
     if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
@@ -408,6 +442,8 @@ int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const 
         size_t nblk = elems / 256;
         if (nbytes != nblk * bb) return fail(ctx, JANUS_E_INVALID_DIM, "K-quant tensor byte size mismatch");
         qs.assign(src, src + nbytes);
+        if (q5)
+            for (size_t b = 0; b < nblk; ++b) q5k_pack_high_bits(qs.data() + b * bb);
         if (ftz)
             for (size_t b = 0; b < nblk; ++b) {
                 uint8_t *blk = qs.data() + b * bb;

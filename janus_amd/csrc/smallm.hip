@@ -730,11 +730,14 @@ __global__ void t32_q5_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq,
     uint8_t out[16] = {0};
     float2 side = make_float2(0.0f, 0.0f);
     if (r < n) {
-        const uint8_t *blk = blocks + ((size_t)r * nsb + sb) * 176, *qh = blk + 16, *qs = blk + 48;
-        // element e of sub-block 2j + hb: nibble hb of qs[32j + e], bit 2j + hb of qh[e]
+        const uint8_t *blk = blocks + ((size_t)r * nsb + sb) * 176, *qs = blk + 48;
+        const uint32_t *qh = (const uint32_t *)(blk + 16);   // one word per 16-byte quant chunk
+        // element e of sub-block 2j + hb: nibble hb of qs[32j + e], its fifth bit
+        // in the word of chunk 2j + e / 16 at bit 8 (t % 4) + t / 4 + 4 hb, t = e % 16
         auto val = [&](int e) -> uint8_t {
             const uint32_t q = (qs[32 * j + e] >> (4 * hb)) & 15u;
-            return (uint8_t)(q | (((uint32_t)(qh[e] >> (2 * j + hb)) & 1u) << 4));
+            const uint32_t t = (uint32_t)e % 16u, pos = 8 * (t % 4) + t / 4 + 4 * hb;
+            return (uint8_t)(q | (((qh[2 * j + e / 16] >> pos) & 1u) << 4));
         };
         for (int e = 0; e < 8; ++e) {
             out[e] = val(8 * h + e);
