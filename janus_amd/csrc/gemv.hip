@@ -719,7 +719,10 @@ __device__ __forceinline__ float reduce_wave_rows(float (&v)[R], int lane, int &
 // stage() fills. XMODE 2: x is read from LDS per unit at every use (long rows,
 // where x in registers would cost occupancy). stage() is called by every
 // wavefront of the workgroup after the first weight loads are issued.
-template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int>
+// DB = false drops the second weight buffer: the next row group is requested
+// only after the current one is reduced (long rows whose registers would
+// otherwise spill, where a wavefront rarely owns more than one group).
+template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int, bool DB = true>
 __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = nullptr,
                                               const float *sx16 = nullptr, StageFn stage = 0) {
     const int lane = threadIdx.x & 63;
@@ -866,7 +869,17 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
 
     uint32_t it = 0, g = wave;
     float2 ra = load_side(g), rb;
-    for (; it + 2 < mine; it += 2, g += 2 * nwaves) {
+    if constexpr (!DB) {
+        for (;;) {
+            consume(wa, g, ra);
+            if (++it >= mine) break;
+            g += nwaves;
+            ra = load_side(g);
+            load(wa, g);
+        }
+        it = mine;   // the double-buffered tail below has nothing left
+    }
+    for (; DB && it + 2 < mine; it += 2, g += 2 * nwaves) {
         rb = load_side(g + nwaves);
         load(wb, g + nwaves);
         consume(wa, g, ra);
@@ -874,7 +887,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
         load(wa, g + 2 * nwaves);
         consume(wb, g + nwaves, rb);
     }
-    if (it + 1 < mine) {
+    if (DB && it + 1 < mine) {
         rb = load_side(g + nwaves);
         load(wb, g + nwaves);
         consume(wa, g, ra);
@@ -1041,8 +1054,13 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
         __syncthreads();
     };
     constexpr int XMODE = BPL <= 4 ? 1 : 2;
-    if (a.units == 64u * BPL) gemv_reg_body<F, _Float16, BPL, R, true, XMODE>(a, xs, sx16, stage);
-    else gemv_reg_body<F, _Float16, BPL, R, false, XMODE>(a, xs, sx16, stage);
+    // long K-quant rows: single-buffered (the 512-thread workgroup caps a lane
+    // at 128 VGPRs, and two buffers of chunks plus headers spill)
+    constexpr bool DB = !(BPL >= 5 && F::XREREAD);
+    if (a.units == 64u * BPL)
+        gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB>(a, xs, sx16, stage);
+    else
+        gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB>(a, xs, sx16, stage);
 }
 
 // Generic fallback for F16 weights whose k is not a multiple of 8: one
