@@ -722,9 +722,11 @@ __device__ __forceinline__ float reduce_wave_rows(float (&v)[R], int lane, int &
 // DB = false drops the second weight buffer: the next row group is requested
 // only after the current one is reduced (long rows whose registers would
 // otherwise spill, where a wavefront rarely owns more than one group).
-template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int, bool DB = true>
+// pre() (if given) runs before the first weight loads are requested.
+template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int, bool DB = true,
+          class PreFn = int>
 __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = nullptr,
-                                              const float *sx16 = nullptr, StageFn stage = 0) {
+                                              const float *sx16 = nullptr, StageFn stage = 0, PreFn pre = 0) {
     const int lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
@@ -753,7 +755,12 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
     };
     const bool has = wave < groups;
     const uint32_t mine = has ? (groups - 1 - wave) / nwaves + 1 : 0;   // groups this wavefront owns
-    if (has) load(wa, wave);
+    if constexpr (!std::is_same<PreFn, int>::value) pre();
+    // Wavefronts without a group (the last workgroup of the LDS kernel) still
+    // request a real one and discard it: every wavefront then issues the same
+    // loads, so the wait for x in stage() counts exactly and does not also
+    // wait for the weights.
+    load(wa, has ? wave : groups - 1);
     if constexpr (XMODE != 0) stage();
     if (!has) return;
 
@@ -940,12 +947,16 @@ __device__ __forceinline__ void store_x16(const float (&v)[16], uint32_t g, _Flo
 // every thread loads its 16-element groups once, with all loads in flight
 // together; the sum of squares is reduced over the workgroup in a fixed order
 // (thread order, then wavefront order), then x * (1 / rms) * gamma is staged.
-template <bool PERM, int MAXG>
-__device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16 *xs, float *sx16,
-                               const float *__restrict__ gamma, float eps, float *red) {
-    const uint32_t g16 = (k + 15) / 16;
-    float v[MAXG][16], gm[MAXG][16];
-    float ss = 0.0f;
+// The loads (norm_load) are requested before the weights: loads return in
+// issue order, so x requested after the weights would hold the reduction and
+// its barriers until every weight load had landed.
+template <int MAXG> struct NormRegs { float v[MAXG][16], gm[MAXG][16]; };
+
+template <int MAXG>
+__device__ __forceinline__ void norm_load(const float *__restrict__ x, const float *__restrict__ gamma, uint32_t k,
+                                          NormRegs<MAXG> &r) {
+    auto &v = r.v;
+    auto &gm = r.gm;
     // x and gamma are requested together: one round trip before the reduction
 #pragma unroll
     for (int j = 0; j < MAXG; ++j) {
@@ -968,6 +979,14 @@ __device__ void stage_x16_norm(const float *__restrict__ x, uint32_t k, _Float16
             }
         }
     }
+}
+
+template <bool PERM, int MAXG>
+__device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, _Float16 *xs, float *sx16, float eps, float *red) {
+    const uint32_t g16 = (k + 15) / 16;
+    auto &v = r.v;
+    const auto &gm = r.gm;
+    float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXG; ++j)
 #pragma unroll
@@ -1045,9 +1064,13 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
     _Float16 *xs = (_Float16 *)smem;
     float *sx16 = (float *)(smem + ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~15u));
     float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
+    NormRegs<NORM_MAXG> nr;
+    auto pre = [&]() {
+        if constexpr (NORM) norm_load<NORM_MAXG>((const float *)a.x, a.gamma, a.k, nr);
+    };
     auto stage = [&]() {
         if constexpr (NORM) {
-            stage_x16_norm<F::PERM, NORM_MAXG>((const float *)a.x, a.k, xs, sx16, a.gamma, a.eps, red);
+            stage_x16_norm<F::PERM, NORM_MAXG>(nr, a.k, xs, sx16, a.eps, red);
         } else {
             stage_x16<F::PERM, false>(a.x, a.k, xs, sx16, nullptr, 1.0f);
         }
@@ -1060,9 +1083,9 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
     // single-buffered (4096x14336: 10.6 against 9.8 us) and keep the prefetch.
     constexpr bool DB = !(BPL >= 5 && F::XREREAD);
     if (a.units == 64u * BPL)
-        gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB>(a, xs, sx16, stage);
+        gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
     else
-        gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB>(a, xs, sx16, stage);
+        gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
 }
 
 // Generic fallback for F16 weights whose k is not a multiple of 8: one

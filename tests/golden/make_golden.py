@@ -1,5 +1,5 @@
 """Writes the golden fixtures in this directory (run from the repository root:
-`python tests/golden/make_golden.py`).
+`python tests/golden/make_golden.py [fixture ...]`).
 
 The reference (Rust + WGSL on wgpu) cannot be built or run in this image, so
 these vectors come from the build's own seeded generators and the CPU oracle
@@ -17,6 +17,11 @@ the same stored bytes from now on:
                 and hd 128 / theta 5e5 (model/transformer/constructor.rs:454-489).
   f16.npz       binary16 -> binary32 decodes of chosen bit patterns in the
                 three reference variants (exact, Q8_0 scale, flush-to-zero).
+  kquant.npz    Q5_K blocks (subnormal d / dmin, every scale bit and every
+                high bit in use) with their dequantised bits (exact and
+                flush-to-zero), Q6_K blocks with their dequantised bits in
+                GGML and in the reference loader's element order
+                (compute/engine.rs:198-248), and 64x256 Q5_K / Q6_K products.
   greedy_c1.npz benchmark configuration 1 (synth.tiny_config1(1)): the 32-token prompt,
                 the 16 greedy tokens under the reference loop and sampler
                 (generation.rs:129-323, sampler.rs:146-209) and the first
@@ -98,11 +103,46 @@ def greedy_c1() -> dict:
             "logits0": np.asarray(logits[0], np.float32)}
 
 
-def main() -> None:
-    for name, fn in (("blocks", blocks), ("gemv", gemv), ("rope", rope), ("f16", f16), ("greedy_c1", greedy_c1)):
-        np.savez_compressed(HERE / f"{name}.npz", **fn())
+def kquant() -> dict:
+    rng = np.random.default_rng(1003)
+    q5k = synth.random_q5_k(rng, 2, 512).reshape(-1, 176)          # 4 super-blocks
+    q5k[0, 0:2] = np.array([0x0003], np.uint16).view(np.uint8)     # subnormal d
+    q5k[1, 2:4] = np.array([0x0200], np.uint16).view(np.uint8)     # subnormal dmin
+    q5k[2, 4:16] = np.arange(12, dtype=np.uint8) * 21              # every bit of the 6-bit packing in use
+    q5k[3, 16:48] = 0xFF                                           # every fifth bit set
+    q6k = synth.random_q6_k(rng, 2, 512).reshape(-1, 210)
+    q6k[0, 192:208] = np.array([-128, 127] * 8, np.int8).view(np.uint8)   # extreme scales
+    q6k[1, 208:210] = np.array([0x0001], np.uint16).view(np.uint8)        # subnormal d
+    q5k, q6k = q5k.reshape(-1), q6k.reshape(-1)
+    out = {
+        "q5_k": q5k, "q5_k_deq_exact": _bits(O.dequant(13, q5k, 2, 512)),
+        "q5_k_deq_ftz": _bits(O.dequant(13, q5k, 2, 512, ftz=True)),
+        "q6_k": q6k, "q6_k_deq_ggml": _bits(O.dequant(14, q6k, 2, 512)),
+        "q6_k_deq_ref": _bits(O.dequant(14, q6k, 2, 512, q6k_ref_order=True)),
+    }
+    n, k = 64, 256
+    out["x"] = rng.standard_normal(k, dtype=np.float32)
+    for name, t, gen in (("q5_k", 13, synth.random_q5_k), ("q6_k", 14, synth.random_q6_k)):
+        raw = gen(rng, n, k)
+        out["gemv_" + name] = raw
+        out["gemv_" + name + "_y"] = O.gemm_auto(out["x"], t, raw, n, k)
+        wf = O.dequant(t, raw, n, k)
+        if t == 14:   # the reference runs Q6_K as flush-to-zero binary16 weights
+            wf = O.f16_to_f32(O.f32_to_f16_rne(wf), "ftz").reshape(n, k)
+        out["gemv_" + name + "_y64"] = O.gemv_f64(wf, out["x"])
+    return out
+
+
+FIXTURES = {"blocks": blocks, "gemv": gemv, "rope": rope, "f16": f16, "kquant": kquant, "greedy_c1": greedy_c1}
+
+
+def main(names: list[str]) -> None:
+    """Writes every fixture, or only the named ones (an existing file is
+    rewritten only when asked for, so unrelated fixtures keep their bytes)."""
+    for name in names or list(FIXTURES):
+        np.savez_compressed(HERE / f"{name}.npz", **FIXTURES[name]())
         print(f"wrote tests/golden/{name}.npz")
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

@@ -46,6 +46,28 @@ def test_gemv_golden():
         assert np.all(np.abs(d[name + "_y"] - d[name + "_y64"]) <= bound), name
 
 
+def test_kquant_golden():
+    d = _load("kquant")
+    assert np.array_equal(_bits(O.dequant(13, d["q5_k"], 2, 512)), d["q5_k_deq_exact"])
+    assert np.array_equal(_bits(O.dequant(13, d["q5_k"], 2, 512, ftz=True)), d["q5_k_deq_ftz"])
+    assert np.array_equal(_bits(O.dequant(14, d["q6_k"], 2, 512)), d["q6_k_deq_ggml"])
+    assert np.array_equal(_bits(O.dequant(14, d["q6_k"], 2, 512, q6k_ref_order=True)), d["q6_k_deq_ref"])
+    # Q5_K with its high bits cleared is the independent numpy Q4_K closed form
+    # of the same header and nibbles
+    b = d["q5_k"].reshape(-1, 176).copy()
+    q4 = np.ascontiguousarray(np.concatenate([b[:, :16], b[:, 48:]], axis=1)).reshape(-1)
+    b[:, 16:48] = 0
+    for ftz in (False, True):
+        assert np.array_equal(_bits(O.dequant(13, b.reshape(-1), 2, 512, ftz=ftz)), _bits(np_q4_k(q4, ftz)))
+    x = d["x"]
+    for name, t in (("q5_k", 13), ("q6_k", 14)):
+        y = O.gemm_auto(x, t, d["gemv_" + name], 64, 256)
+        assert np.array_equal(_bits(y), _bits(d["gemv_" + name + "_y"])), name
+        wf = O.dequant(t, d["gemv_" + name], 64, 256)
+        bound = 1e-5 * (np.abs(wf.astype(np.float64)) @ np.abs(x.astype(np.float64))) + 1e-30
+        assert np.all(np.abs(d["gemv_" + name + "_y"] - d["gemv_" + name + "_y64"]) <= 2 * bound), name
+
+
 def test_rope_golden_and_closed_form():
     d = _load("rope")
     for key, hd, theta in (("hd64_theta1e4", 64, 10000.0), ("hd128_theta5e5", 128, 500000.0)):

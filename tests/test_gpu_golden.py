@@ -40,6 +40,27 @@ def test_gpu_gemv_matches_golden(engine):
         assert np.all(np.abs(y.cpu().numpy() - d[name + "_y64"]) <= bound), name
 
 
+def test_gpu_kquant_matches_golden(engine):
+    d = np.load(G / "kquant.npz")
+    from oracle import oracle as O
+    for flags, key in ((0, "q5_k_deq_exact"), (1, "q5_k_deq_ftz")):
+        w = ops.GpuTensor(engine, 13, 2, 512, d["q5_k"], flags)
+        assert np.array_equal(_bits(w.dequant().cpu().numpy()), d[key]), key
+    # Q6_K is stored as the binary16 rounding of its dequantisation
+    for flags, key in ((0, "q6_k_deq_ggml"), (2, "q6_k_deq_ref")):
+        w = ops.GpuTensor(engine, 14, 2, 512, d["q6_k"], flags)
+        want = O.f16_to_f32(O.f32_to_f16_rne(d[key].view(np.float32)), "exact")
+        assert np.array_equal(_bits(w.dequant().cpu().numpy()), _bits(want)), key
+    x = torch.from_numpy(d["x"]).to(DEV)
+    for name, t, flags in (("q5_k", 13, 0), ("q6_k", 14, 1)):
+        w = ops.GpuTensor(engine, t, 64, 256, d["gemv_" + name], flags)
+        y = torch.empty(64, device=DEV)
+        ops.gemm_auto(engine, x, w, y, 1, 1, 256, 64)
+        wf = w.dequant().cpu().numpy().astype(np.float64)
+        bound = 1e-5 * (np.abs(wf) @ np.abs(d["x"].astype(np.float64))) + 1e-30
+        assert np.all(np.abs(y.cpu().numpy() - d["gemv_" + name + "_y64"]) <= bound), name
+
+
 def test_gpu_rope_table_matches_golden(engine):
     d = np.load(G / "rope.npz")
     for key, hd, theta in (("hd64_theta1e4", 64, 10000.0), ("hd128_theta5e5", 128, 500000.0)):
