@@ -1199,15 +1199,18 @@ int launch_reg_fmt(janus_ctx *ctx, const GemvArgs &a, bool &done) {
 // compiled kernel), each wavefront walking several row groups.
 template <class F, int BPL, int R>
 int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
-    static int per_cu[2] = {0, 0};
+    // resident workgroups per CU for this kernel at this LDS size (4 KB steps)
+    static int per_cu[2][17] = {};
     const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
     const uint32_t nblk = (a.k + XB - 1) / XB;
     const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
-    int &occ = per_cu[norm ? 1 : 0];
+    const size_t lds_step = (lds + 4095) / 4096;
+    int &occ = per_cu[norm ? 1 : 0][lds_step];
     if (occ == 0) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 512, 40 * 1024) != hipSuccess || nb < 1) nb = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 512, lds_step * 4096) != hipSuccess || nb < 1)
+            nb = 1;
         occ = nb;
     }
     const int wg_cap = (int)ctx->gemv_lds_wpc / 8;   // 8 wavefronts per workgroup
