@@ -81,8 +81,11 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
-@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008)])
+@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
+    """(1003, 8704): the LDS-staged kernel with five units per lane (the
+    single-buffered body for K-quants, double-buffered otherwise) and a last
+    workgroup whose five idle wavefronts stream a real row group and discard it."""
     raw, w = _weight(engine, ggml_type, n, k, 3 * n + k, FTZ[ggml_type])
     rng = np.random.default_rng(n)
     xh = rng.standard_normal(k).astype(np.float16)
