@@ -1009,6 +1009,45 @@ __device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, _Float16 *xs, floa
     }
 }
 
+// binary16 x of the plain (not normalised) LDS staging, requested before the
+// weights like norm_load: every thread's groups of 16 (k <= 16 * 512 * 2)
+// held in registers until the weights are in flight.
+struct X16Regs { uint4 u[2][2]; };
+
+__device__ __forceinline__ void x16_load(const _Float16 *__restrict__ x, uint32_t k, X16Regs &r) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t e0 = (threadIdx.x + 512u * j) * 16;
+        const bool full = e0 + 16 <= k;
+        r.u[j][0] = full ? *(const uint4 *)(x + e0) : make_uint4(0u, 0u, 0u, 0u);
+        r.u[j][1] = full ? *(const uint4 *)(x + e0 + 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+template <bool PERM>
+__device__ void x16_store(const X16Regs &r, const _Float16 *__restrict__ x, uint32_t k, _Float16 *xs, float *sx16) {
+    const uint32_t g16 = (k + 15) / 16;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t g = threadIdx.x + 512u * j, e0 = g * 16;
+        if (g >= g16) continue;
+        float v[16];
+        if (e0 + 16 <= k) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const uint4 u = r.u[j][q];
+                const jh2 h[4] = {as_h2(u.x), as_h2(u.y), as_h2(u.z), as_h2(u.w)};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) { v[8 * q + 2 * t] = (float)h[t].x; v[8 * q + 2 * t + 1] = (float)h[t].y; }
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) v[t] = e0 + t < k ? (float)x[e0 + t] : 0.0f;
+        }
+        store_x16<PERM>(v, g, xs, sx16);
+    }
+}
+
 // Vectorised staging of binary16 x for the LDS kernel: each thread handles
 // groups of 16 elements (16-byte global loads of x, and of gamma when
 // normalising) and writes them with 8-byte LDS stores in the layout of
@@ -1065,23 +1104,34 @@ __global__ __launch_bounds__(512) void gemv_lds_kernel(GemvArgs a) {
     float *sx16 = (float *)(smem + ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~15u));
     float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
     NormRegs<NORM_MAXG> nr;
+    // long Q4_0 / Q8_0 rows without the norm: x requested first as well, in
+    // the registers the single-buffered body leaves free
+    constexpr bool XPRE = !NORM && BPL >= 5 && !F::XREREAD && !std::is_same<F, FF16>::value;
+    X16Regs xr;
+    const bool xpre = XPRE && a.k <= 16u * 512u * 2u;
     auto pre = [&]() {
         if constexpr (NORM) norm_load<NORM_MAXG>((const float *)a.x, a.gamma, a.k, nr);
+        if constexpr (XPRE)
+            if (xpre) x16_load((const _Float16 *)a.x, a.k, xr);
     };
     auto stage = [&]() {
         if constexpr (NORM) {
             stage_x16_norm<F::PERM, NORM_MAXG>(nr, a.k, xs, sx16, a.eps, red);
+        } else if (XPRE && xpre) {
+            x16_store<F::PERM>(xr, (const _Float16 *)a.x, a.k, xs, sx16);
         } else {
             stage_x16<F::PERM, false>(a.x, a.k, xs, sx16, nullptr, 1.0f);
         }
         __syncthreads();
     };
     constexpr int XMODE = BPL <= 4 ? 1 : 2;
-    // long K-quant rows: single-buffered (the 512-thread workgroup caps a lane
-    // at 128 VGPRs, and two buffers of chunks plus headers spill; at these
-    // shapes a wavefront owns one row group). Q4_0 rows measured slower
-    // single-buffered (4096x14336: 10.6 against 9.8 us) and keep the prefetch.
-    constexpr bool DB = !(BPL >= 5 && F::XREREAD);
+    // long rows single-buffered (the 512-thread workgroup caps a lane at 128
+    // VGPRs; at these shapes a wavefront owns one row group): K-quants, whose
+    // two buffers of chunks plus headers spill, and long Q4_0 / Q8_0 rows,
+    // which spend the freed registers on x requested before the weights
+    // (single-buffered alone measured slower: 4096x14336 10.6 against 9.8 us;
+    // with x first 9.05 us)
+    constexpr bool DB = !(BPL >= 5 && F::XREREAD) && !XPRE;
     if (a.units == 64u * BPL)
         gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
     else
