@@ -19,8 +19,17 @@ Workload (headline metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
     dense fp16 MFMA peak.
   * llama2_7b_q4k_c3: config 3 (Llama-2-7B shape, Q4_K, decode to 2048 ctx).
   * attention_c4: config 4 (16 ragged sequences, GQA 32/8, fp16 KV).
+  * bs1_penalty / bs1_reference_dtype: the same batch-1 decode with the
+    reference's default greedy sampler in the captured step (repetition
+    penalty 1.15 over the generated tokens, last-max argmax), and with the
+    reference's dtypes (f32 activations into the products, f32 KV).
+  * in_step: per-kernel HBM fractions inside the batch-1 decode step, from the
+    kernel trace committed in profiles/ (bytes computed here from the shapes).
   * cpu_baseline: the CPU oracle (a restatement of the reference arithmetic, not
-    the reference itself) on the same model, one thread, a bounded sample.
+    the reference itself) on the same model, OpenMP over rows on every host
+    core, median per-token time of a bounded sample.
+
+Every timed leg reports the median of its trials.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -40,11 +49,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0    # dense fp16 MFMA, MI355X
-# HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE passes of `bench.py --only roofline`, FETCH_SIZE scaled by 2.0 and
-# WRITE_SIZE by 1.0 (the factors a 1 GiB device copy gives on this device);
-# recorded in profiles/gemv_q4_0_14336x4096_f16.md. Re-measure when the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 33366077
+PROFILES = ROOT / "profiles"
 METRIC = "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 & 32; GEMV HBM GB/s vs peak"
 L3 = dict(hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256, layers=32, rope_theta=500000.0)
 
@@ -53,31 +58,65 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def profile_record(name: str) -> dict | None:
+    """The machine-readable block (a ```json fence) of profiles/<name>.md: the
+    figures a rocprofv3 run gave, with the commit it ran at."""
+    path = PROFILES / f"{name}.md"
+    if not path.exists():
+        return None
+    text = path.read_text()
+    start = text.find("```json")
+    if start < 0:
+        return None
+    end = text.find("```", start + 7)
+    return json.loads(text[start + 7:end])
+
+
+def median_ms(run, trials: int = 5) -> float:
+    """Median over `trials` of HIP-event time (ms) around run() on torch's
+    current stream (where every timed launch here is enqueued)."""
+    import torch
+    times = []
+    for _ in range(trials):
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        run()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return float(np.median(times))
+
+
 def llama3_spec(seed: int, layers: int = 32):
     from janus_amd import synth
     return synth.make_model(seed, L3["hidden"], L3["heads"], L3["kv_heads"], L3["ffn"], L3["vocab"], layers,
                             synth.Q4_0, 1e-5, L3["rope_theta"], embed_type=synth.F16, head_type=synth.F16)
 
 
-def decode_bs1(engine, spec, steps: int, warmup: int, prompt_len: int = 128):
-    import torch
+def decode_bs1(engine, spec, steps: int, warmup: int, prompt_len: int = 128, penalty: float | None = None,
+               f32: bool = False, trials: int = 5):
+    """Batch-1 greedy decode: prefill token by token, then `steps` captured
+    decode steps per trial (the median of `trials` is returned, in ms for the
+    `steps` steps). penalty: the reference's default sampler in the captured
+    step (repetition penalty over the generated tokens, last-max argmax);
+    otherwise plain last-max argmax. f32: the reference's dtypes (f32
+    activations into the products, f32 KV)."""
     from janus_amd import _lib
     from janus_amd.model import Model
-    max_seq = prompt_len + warmup + steps + 8
-    m = Model(engine, spec, max_seq_len=max_seq, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    max_seq = prompt_len + warmup + trials * steps + 8
+    dt = _lib.DT_F32 if f32 else _lib.DT_F16
+    m = Model(engine, spec, max_seq_len=max_seq, kv_dtype=dt, act_dtype=dt)
     rng = np.random.default_rng(5)
     prompt = rng.integers(0, spec.vocab, prompt_len).tolist()
     for p, t in enumerate(prompt):           # prefill token by token (generation.rs:161-173)
         m.forward([t], [p])
+    if penalty is not None:
+        m.set_sampler(_lib.SAMPLER_PENALTY, penalty)
     m.graph_begin([prompt[-1]], [prompt_len])
     m.graph_run(warmup)
     engine.sync()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    m.graph_run(steps)
-    e.record()
-    e.synchronize()
-    ms = s.elapsed_time(e)
+    ms = median_ms(lambda: m.graph_run(steps), trials)
     toks = m.graph_tokens(1)
     m.close()
     return ms, toks
@@ -145,13 +184,15 @@ def decode_c3(engine, spec, prompt_len: int = 512, ctx: int = 2048):
     return ms, steps - 1, prefill_s
 
 
-def decode_bs32(engine, spec, steps: int, warmup: int):
+def decode_bs32(engine, spec, steps: int, warmup: int, trials: int = 5):
+    """Config 5: 32 sequences over random fp16 caches at contexts U[256, 4096],
+    captured ragged steps; median of `trials` timed runs of `steps` steps (ms)."""
     import torch
     from janus_amd import _lib
     from janus_amd.model import Model
     rng = np.random.default_rng(5)
     lens = rng.integers(256, 4097, 32)
-    max_seq = int(lens.max()) + warmup + steps + 8
+    max_seq = int(lens.max()) + warmup + trials * steps + 8
     m = Model(engine, spec, max_seq_len=max_seq, max_batch=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
     shape = (spec.layers, 32 * max_seq, spec.kv_heads, spec.head_dim)
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -162,12 +203,7 @@ def decode_bs32(engine, spec, steps: int, warmup: int):
     m.graph_begin(toks, lens.tolist())
     m.graph_run(warmup)
     engine.sync()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    m.graph_run(steps)
-    e.record()
-    e.synchronize()
-    ms = s.elapsed_time(e)
+    ms = median_ms(lambda: m.graph_run(steps), trials)
     m.close()
     del k, v
     return ms, int(lens.sum())
@@ -211,15 +247,7 @@ def gemv_roofline(engine, n: int = 14336, k: int = 4096, launches: int = 200, qt
     engine.bind_stream()
     graph.replay()
     torch.cuda.synchronize()
-    best = 1e30
-    for _ in range(5):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        graph.replay()
-        e.record()
-        e.synchronize()
-        best = min(best, s.elapsed_time(e))
-    us = best * 1e3 / launches
+    us = median_ms(graph.replay) * 1e3 / launches
     algo = nbytes + 2 * k + 2 * n     # weights once, x in, y out (fp16)
     del graph, ws
     return us, algo, copies
@@ -251,16 +279,9 @@ def gemm_m32(engine, n: int, k: int, rows: int = 32, launches: int = 100, qtype:
     engine.bind_stream()
     graph.replay()
     torch.cuda.synchronize()
-    best = 1e30
-    for _ in range(5):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        graph.replay()
-        e.record()
-        e.synchronize()
-        best = min(best, s.elapsed_time(e))
+    us = median_ms(graph.replay) * 1e3 / launches
     del graph, ws
-    return best * 1e3 / launches, raw.nbytes + 2 * rows * k + 2 * rows * n, 2.0 * rows * n * k
+    return us, raw.nbytes + 2 * rows * k + 2 * rows * n, 2.0 * rows * n * k
 
 
 def attention_c4(engine, reps: int = 20):
@@ -285,18 +306,14 @@ def attention_c4(engine, reps: int = 20):
                                          seq_lens=d_lens, max_len_hint=int(lens.max()))
     call()
     torch.cuda.synchronize()
-    best = 1e30
-    for _ in range(5):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
+
+    def run():
         for _ in range(reps):
             call()
-        e.record()
-        e.synchronize()
-        best = min(best, s.elapsed_time(e) / reps)
+    us = median_ms(run) * 1e3 / reps
     algo = rows * 8 * 128 * 2 * 2 + q.numel() * 4 + out.numel() * 4
     del k, v
-    return best * 1e3, algo, rows
+    return us, algo, rows
 
 
 def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10):
@@ -308,30 +325,53 @@ def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10):
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    best = 1e30
-    for _ in range(reps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        dst.copy_(src)
-        e.record()
-        e.synchronize()
-        best = min(best, s.elapsed_time(e))
+    ms = median_ms(lambda: dst.copy_(src), reps)
     del src, dst
-    return 2 * nbytes / (best * 1e-3) / 1e9
+    return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(spec, tokens: int = 2):
-    """The oracle (CPU restatement of the reference path), single thread, on a
-    bounded sample: `tokens` decode tokens at positions 0.. of the same model."""
+def cpu_baseline(spec, tokens: int = 20):
+    """The oracle (CPU restatement of the reference path, products OpenMP over
+    rows on every host core) on a bounded sample: `tokens` greedy decode
+    tokens at positions 0.. of the same model, each timed alone; returns
+    (tok/s from the median token time, threads, total seconds)."""
     from oracle import oracle as O
-    m = O.OracleModel(spec, max_seq_len=16, kv_f16=True)
-    t0 = time.perf_counter()
+    m = O.OracleModel(spec, max_seq_len=tokens + 1, kv_f16=True)
+    times = []
     tok = 1
     for p in range(tokens):
+        t0 = time.perf_counter()
         logits = m.forward(tok, p)
         tok = O.argmax_last(logits)
-    dt = time.perf_counter() - t0
-    return tokens / dt, dt
+        times.append(time.perf_counter() - t0)
+    return 1.0 / float(np.median(times)), int(O.lib().jo_num_threads()), float(sum(times))
+
+
+def in_step_fractions(prompt_len: int = 128) -> dict | None:
+    """Per-kernel HBM fractions of the batch-1 decode step from the committed
+    kernel trace (profiles/decode_bs1_llama3_8b_q4_0.md): average launch time
+    of each role there, algorithmic bytes from the Llama-3-8B shapes here."""
+    rec = profile_record("decode_bs1_llama3_8b_q4_0")
+    if not rec or "roles" not in rec:
+        return None
+    h, f, kvd, v = L3["hidden"], L3["ffn"], L3["kv_heads"] * 128, L3["vocab"]
+    q40 = lambda n, k: n * k * 18 // 32
+    ctx = rec.get("mean_ctx", prompt_len)
+    algo = {
+        "qkv": q40(h + 2 * kvd, h) + 4 * h + 4 * h + 2 * 2 * kvd,        # weights, f32 x + gamma, K/V append
+        "o_proj": q40(h, h) + 2 * h + 4 * h + 4 * h,                      # weights, f16 x, f32 resid in / out
+        "gate_up": q40(2 * f, h) + 4 * h + 4 * h + 2 * f,
+        "down": q40(h, f) + 2 * f + 4 * h + 4 * h,
+        "attention": 2 * 2 * kvd * ctx + 4 * h + 2 * h,                 # K and V rows once, q in, out
+        "lm_head": 2 * v * h + 4 * h + 4 * h + 4 * v,
+    }
+    out = {"source": "profiles/decode_bs1_llama3_8b_q4_0.md", "commit": rec.get("commit")}
+    for role, us in rec["roles"].items():
+        if role in algo:
+            gbs = algo[role] / us / 1e3
+            out[role] = {"us": round(us, 2), "bytes": algo[role], "GB_s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def main() -> int:
@@ -372,7 +412,7 @@ def main() -> int:
     gemm = None
     if args.only in ("all", "gemm"):
         gemm = {}
-        for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)):
+        for n, k in ((14336, 4096), (6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)):
             u, b, fl = gemm_m32(engine, n, k)
             gemm[f"{n}x{k}"] = {"us_per_launch": round(u, 2), "GB_s": round(b / u / 1e3, 1),
                                 "TFLOP_s": round(fl / u / 1e6, 1), "mfma_frac": round(fl / u / 1e6 / MFMA_PEAK_TFLOPS, 4)}
@@ -437,15 +477,25 @@ def main() -> int:
         ms32, ctx_sum = decode_bs32(engine, spec, args.steps, args.warmup)
         log(f"bs=32 ragged: {ms32 / args.steps:.3f} ms/step, {32 * args.steps / (ms32 / 1e3):.1f} tok/s")
         return 0
-    ms, toks = decode_bs1(engine, spec, args.steps, args.warmup)
+    # the headline: exactly K timed steps after W warmup steps
+    ms, toks = decode_bs1(engine, spec, args.steps, args.warmup, trials=1)
     tok_s = args.steps / (ms / 1e3)
-    log(f"bs=1: {ms / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    log(f"bs=1: {ms / args.steps:.3f} ms/token, {tok_s:.1f} tok/s ({args.steps} timed steps)")
     if args.only == "bs1":
         return 0
+    msp, _ = decode_bs1(engine, spec, args.steps, args.warmup, penalty=1.15)
+    bs1_pen = {"tok_s": round(args.steps / (msp / 1e3), 2), "ms_per_token": round(msp / args.steps, 4),
+               "sampler": "repetition penalty 1.15 over the generated tokens + last-max argmax, in the captured step"}
+    log(f"bs=1 penalty 1.15: {msp / args.steps:.3f} ms/token, {bs1_pen['tok_s']} tok/s")
+    msr, _ = decode_bs1(engine, spec, max(10, args.steps // 4), args.warmup, f32=True)
+    nref = max(10, args.steps // 4)
+    bs1_ref = {"tok_s": round(nref / (msr / 1e3), 2), "ms_per_token": round(msr / nref, 4),
+               "dtypes": "f32 activations into the products, f32 KV (the reference's), plain argmax"}
+    log(f"bs=1 reference dtypes: {msr / nref:.3f} ms/token, {bs1_ref['tok_s']} tok/s")
 
     bs32 = None
     if not args.no_bs32:
-        steps32 = max(5, args.steps // 10)
+        steps32 = max(10, args.steps // 10)
         ms32, ctx_sum = decode_bs32(engine, spec, steps32, 3)
         bs32 = {"tok_s": round(32 * steps32 / (ms32 / 1e3), 1), "ms_per_step": round(ms32 / steps32, 3),
                 "steps": steps32, "ctx_sum": ctx_sum}
@@ -453,11 +503,15 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("cpu baseline: oracle, 1 thread, 2 decode tokens")
-        v, dt = cpu_baseline(spec)
-        cpu = {"value": round(v, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-               "sample": f"2 decode tokens (positions 0-1) of the same Llama-3-8B-shape Q4_0 model through "
-                         f"the C oracle, single thread, {dt:.1f} s"}
+        log("cpu baseline: oracle, OpenMP over rows, 20 decode tokens")
+        v, threads, dt = cpu_baseline(spec)
+        cpu = {"value": round(v, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"20 greedy decode tokens (positions 0-19) of the same Llama-3-8B-shape Q4_0 model "
+                         f"through the C oracle (a restatement of the reference arithmetic, not the reference), "
+                         f"products OpenMP over rows on {threads} threads; median token time of the 20, "
+                         f"{dt:.1f} s in all"}
+    in_step = in_step_fractions()
+    rec = profile_record("gemv_q4_0_14336x4096_f16") or {}
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -468,12 +522,16 @@ def main() -> int:
                                "F16 LM head, HIP-graph decode step", "layers": args.layers,
                    "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
-                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0) per launch, "
-                                       "profiles/gemv_q4_0_14336x4096_f16.md",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": rec.get("traffic_bytes"),
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per launch, scaled by a "
+                                       "device copy's counts (profiles/gemv_q4_0_14336x4096_f16.md, commit "
+                                       f"{rec.get('commit')})",
                      "kernel": "Q4_0 GEMV 14336x4096 (x fp16, y fp16)", "us_per_launch": round(us, 3),
                      "algorithmic_bytes": algo, "other_shapes": shapes, "device_copy_GB_s": round(copy_gbs, 1)},
         "bs32": bs32,
+        "bs1_penalty": bs1_pen,
+        "bs1_reference_dtype": bs1_ref,
+        "in_step": in_step,
         "gemm_m32_q4_0": gemm,
         "kquant": kq,
         "llama2_7b_q4k_c3": c3,

@@ -84,6 +84,11 @@ int janus_abi_version(void);
 int janus_set_stream(janus_ctx *ctx, void *hip_stream);
 void *janus_get_stream(janus_ctx *ctx);
 int janus_sync(janus_ctx *ctx);                      /* device.poll(wait) */
+/* Current sizes of the context's attention and small-M GEMM workspaces (the
+ * library-owned split-K partials; diagnostics, no reference counterpart).
+ * A workspace that grows keeps its old buffer until janus_destroy, because a
+ * captured HIP graph may still use it. */
+int janus_workspace_bytes(const janus_ctx *ctx, size_t *attn_bytes, size_t *gemm_bytes);
 int janus_device_count(int *count);
 /* Buffer helpers for callers without their own allocator (Buffer,
  * compute/buffer.rs): plain device memory. */

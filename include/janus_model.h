@@ -60,27 +60,69 @@ int janus_model_reset(janus_model *m);
 int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_each);
 /* One decode step for nseq sequences: sequence s consumes tokens[s] at
  * position positions[s] (its KV rows start at s * max_seq_len). Logits land
- * in janus_model_logits()[s][vocab]. */
+ * in janus_model_logits()[s][vocab]. Model::forward_batch
+ * (model/transformer/forward.rs:141-245), with a position per sequence. */
 int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq);
+/* As janus_model_forward, with sequence s in KV slot slots[s] (its rows start
+ * at slots[s] * max_seq_len; slots distinct, each < max_batch): a sequence
+ * keeps its cache wherever it sits in the batch, so sequences can join and
+ * leave a batch without copying KV. */
+int janus_model_forward_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
+                              const uint32_t *slots, uint32_t nseq);
 const float *janus_model_logits(const janus_model *m);        /* device pointer */
 void *janus_model_kv_cache(const janus_model *m, int which);  /* 0 = K, 1 = V; [layers][rows][kvh][hd] */
 int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq);
 /* Greedy generation with the reference's loop semantics (generation.rs:129-323):
  * prefill token by token, then re-feed the last prompt token at position n
- * and sample with the repetition penalty over generated tokens and the
- * last-max argmax (model/sampler.rs:146-209,599-613,784-795). Stops at
- * max_tokens, at 128001/128009 (generation.rs:241-260) or at max_seq_len. */
+ * and sample as Sampler::sample does with temperature 0 (model/sampler.rs:
+ * 146-209): with |repetition_penalty - 1| < 0.01 the GPU argmax and its tie
+ * rule (shaders/argmax.wgsl:26-126), otherwise the penalty over the generated
+ * tokens (:599-613) and the last-max argmax (:784-795). Stops at max_tokens,
+ * at max_seq_len, or at 128001/128009 (generation.rs:241-260; the stop token
+ * is not returned, as the reference does not push it). Runs on the device:
+ * the decode step is captured once and replayed, the penalty's context is
+ * kept as occurrence counts on the device and the sampled tokens are read
+ * back in chunks. Sets the model's sampler (janus_model_set_sampler). */
 int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
                          float repetition_penalty, uint32_t *out_tokens, uint32_t *n_out);
+/* Model::generate_batch (generation.rs:673-870) with continuous batching:
+ * request i is prompt_lens[i] token ids, the prompts back to back in
+ * `prompts`. Up to max_batch requests run at once, each in its own KV slot
+ * and at its own position (prefill token by token, then the re-fed last
+ * prompt token, then decode). A request leaves when it has max_tokens
+ * tokens, hits 128001/128009 (kept in its output, as the reference pushes
+ * it before the check, generation.rs:810-833) or fills max_seq_len, and a
+ * waiting request takes its slot without any KV copy. Sampling follows
+ * Sampler::sample_batch (sampler.rs:379-428): the penalty over that
+ * request's generated tokens, then the last-max argmax. Output: request i's
+ * tokens at out_tokens[i * max_tokens], n_out[i] of them. Sets the model's
+ * sampler. */
+int janus_model_generate_batch(janus_model *m, const uint32_t *prompts, const uint32_t *prompt_lens, uint32_t nreq,
+                               uint32_t max_tokens, float repetition_penalty, uint32_t *out_tokens, uint32_t *n_out);
+
+/* Greedy rule of the device-side decode step (graph decode, generate). */
+#define JANUS_SAMPLER_ARGMAX 0   /* last maximal logit, no penalty */
+#define JANUS_SAMPLER_PENALTY 1  /* repetition penalty over the generated tokens, then last-max
+                                    (sampler.rs:599-613, 784-795) */
+#define JANUS_SAMPLER_WGSL 2     /* no penalty, the tie rule of shaders/argmax.wgsl:26-126 */
+int janus_model_set_sampler(janus_model *m, int mode, float repetition_penalty);
 
 /* Graph decode: capture one greedy decode step (embed from device ids ->
- * forward -> argmax written back as the next ids, positions advanced on the
- * device) for nseq sequences, then replay it `steps` times. Device state:
- * janus_model_device_tokens() [nseq] int32, janus_model_device_positions()
- * [nseq] int32, initialised by janus_model_graph_begin. */
+ * forward -> greedy choice under the model's sampler written back as the next
+ * ids, positions advanced on the device) for nseq sequences once, then replay
+ * it `steps` times. janus_model_graph_begin sets sequence s to token
+ * tokens[s] at position positions[s] in KV slot s (or slots[s]) and clears
+ * its generated tokens. A captured step is kept per sequence count and
+ * reused until a tensor or the KV cache is replaced. */
 int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq);
+int janus_model_graph_begin_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
+                                  const uint32_t *slots, uint32_t nseq);
 int janus_model_graph_run(janus_model *m, uint32_t steps);
+/* The token each sequence consumes next (the last one chosen). */
 int janus_model_graph_read_tokens(janus_model *m, uint32_t *h_tokens, uint32_t nseq);
+/* The tokens generated so far by batch row `row` since its graph_begin or
+ * admission: up to cap of them into h_tokens, their total in *n. */
+int janus_model_read_generated(janus_model *m, uint32_t row, uint32_t *h_tokens, uint32_t cap, uint32_t *n);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,9 @@ WEIGHT_FTZ_F16 = 0x1
 WEIGHT_Q6K_REF_ORDER = 0x2
 TIE_LAST = 0
 TIE_WGSL = 1
+SAMPLER_ARGMAX = 0
+SAMPLER_PENALTY = 1
+SAMPLER_WGSL = 2
 
 P = C.c_void_p
 U32 = C.c_uint32
@@ -65,6 +68,7 @@ _SIGNATURES = {
     "janus_set_stream": (I32, [P, P]),
     "janus_get_stream": (P, [P]),
     "janus_sync": (I32, [P]),
+    "janus_workspace_bytes": (I32, [P, C.POINTER(SZ), C.POINTER(SZ)]),
     "janus_device_count": (I32, [C.POINTER(I32)]),
     "janus_alloc": (I32, [P, SZ, C.POINTER(P)]),
     "janus_free": (I32, [P, P]),
@@ -99,13 +103,18 @@ _SIGNATURES = {
     "janus_model_reset": (I32, [P]),
     "janus_model_set_kv_cache": (I32, [P, P, P, SZ]),
     "janus_model_forward": (I32, [P, P, P, U32]),
+    "janus_model_forward_slots": (I32, [P, P, P, P, U32]),
     "janus_model_logits": (P, [P]),
     "janus_model_kv_cache": (P, [P, I32]),
     "janus_model_read_logits": (I32, [P, P, U32]),
     "janus_model_generate": (I32, [P, P, U32, U32, F32, P, P]),
+    "janus_model_generate_batch": (I32, [P, P, P, U32, U32, F32, P, P]),
+    "janus_model_set_sampler": (I32, [P, I32, F32]),
     "janus_model_graph_begin": (I32, [P, P, P, U32]),
+    "janus_model_graph_begin_slots": (I32, [P, P, P, P, U32]),
     "janus_model_graph_run": (I32, [P, U32]),
     "janus_model_graph_read_tokens": (I32, [P, P, U32]),
+    "janus_model_read_generated": (I32, [P, U32, P, U32, P]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

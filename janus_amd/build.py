@@ -4,7 +4,7 @@ The library is compiled with hipcc for gfx950 only, one object per source
 file in parallel, then linked as a shared object next to this package so the
 GPU box loads it straight from the repository tree.
 
-Usage: python -m janus_amd.build [--jobs N] [--no-oracle]
+Usage: python -m janus_amd.build [--jobs N] [--no-oracle] [--incremental]
 """
 from __future__ import annotations
 
@@ -52,15 +52,28 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build_library(jobs: int | None = None, verbose: bool = True) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libjanus_hip.so."""
+def _stale(src: Path) -> bool:
+    """An object is stale when it is missing or older than its source or any
+    shared header."""
+    obj = BUILD / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.h"), *(ROOT / "include").glob("*.h")]
+    return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
+
+
+def build_library(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libjanus_hip.so
+    (incremental: only sources whose object is stale)."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
-    jobs = jobs or min(8, len(srcs), os.cpu_count() or 1)
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    jobs = jobs or min(8, max(1, len(todo)), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        list(ex.map(_compile, todo))
+    objs = [BUILD / (s.stem + ".o") for s in srcs]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -87,8 +100,9 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--no-oracle", action="store_true")
+    ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
     args = ap.parse_args(argv)
-    build_library(args.jobs)
+    build_library(args.jobs, incremental=args.incremental)
     if not args.no_oracle:
         build_oracle()
     return 0

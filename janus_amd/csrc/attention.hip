@@ -666,18 +666,24 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     *splits_out = (uint32_t)((max_len + chunk * nw - 1) / (chunk * nw));
 }
 
-int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
-                      uint32_t max_len, int kv_f16) {
+size_t attention_ws_bytes(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                          uint32_t max_len, int kv_f16) {
     uint32_t chunk, nw, splits, qh;
     attention_plan(ctx, batch, heads, kv_heads, max_len, kv_f16, &chunk, &nw, &splits, &qh);
-    if (splits <= 1) return JANUS_OK;
-    return ensure_attn_ws(ctx, (size_t)batch * heads * splits * (hd + 2) * sizeof(float));
+    if (splits <= 1) return 0;
+    return (size_t)batch * heads * splits * (hd + 2) * sizeof(float);
+}
+
+int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                      uint32_t max_len, int kv_f16) {
+    const size_t bytes = attention_ws_bytes(ctx, batch, heads, kv_heads, hd, max_len, kv_f16);
+    return bytes ? ensure_attn_ws(ctx, bytes) : JANUS_OK;
 }
 
 int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
                      uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
-                     float scale, int out_f16) {
+                     float scale, int out_f16, float *fixed_ws, size_t fixed_ws_bytes) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -702,8 +708,16 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.ws = nullptr;
     if (splits > 1) {
         size_t bytes = (size_t)batch * heads * splits * (hd + 2) * sizeof(float);
-        if (int e = ensure_attn_ws(ctx, bytes)) return e;
-        a.ws = (float *)ctx->attn_ws;
+        if (fixed_ws) {
+            if (bytes > fixed_ws_bytes)
+                return fail(ctx, JANUS_E_INVALID_DIM,
+                            "attention: split partials need " + std::to_string(bytes) + " bytes, above the " +
+                                std::to_string(fixed_ws_bytes) + "-byte fixed scratch");
+            a.ws = fixed_ws;
+        } else {
+            if (int e = ensure_attn_ws(ctx, bytes)) return e;
+            a.ws = (float *)ctx->attn_ws;
+        }
     }
     const uint32_t G = heads / kv_heads;
     if (kv_dt == JANUS_DT_F16) {

@@ -592,17 +592,20 @@ struct GemvArgs {
     const void *x;       // activation [k]
     void *y;             // output [n] (EPI_SWIGLU: [n / 2])
     const float *resid;  // residual [n] (EPI_RESIDUAL)
-    unsigned long long *best;   // EPI_ARGMAX: running max of argmax_key, reset by the consumer
+    unsigned long long *best;   // EPI_ARGMAX: running max of sampler_key, reset by the consumer
+    const uint32_t *counts;     // EPI_ARGMAX: occurrence counts of generated tokens (SAMPLE_PENALTY), or null
+    const SamplerDev *sampler;  // EPI_ARGMAX: sampler state, or null for SAMPLE_ARGMAX
     uint32_t n, k;
     uint32_t units;      // units per row
     int out_f16;
     int epi;
     // EPI_QKV_ROPE: row pairs are (i, i + hd/2) of a q head, then of a k head,
     // then consecutive v elements; q is rotated into y (f32), k is rotated and
-    // v copied into the cache row of position d_pos[0].
+    // v copied into the cache row d_rowbase[0] + d_pos[0] (d_rowbase may be null).
     void *kc, *vc;
     const float *rope;
     const int32_t *d_pos;
+    const int32_t *d_rowbase;
     uint32_t q_pairs, k_pairs, half_hd, kv_row;
     int kv_f16;
     // fused RMSNorm of x (f32) with gamma, eps (the LDS kernel)
@@ -777,6 +780,13 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
     const int my_ridx = R == 1 ? 0 : R == 2 ? (lane >> 5) : (((lane >> 5) << 1) | ((lane >> 4) & 1));
     const bool writer = (lane & (64 / R - 1)) == 0;
     const uint32_t pos = (a.epi == EPI_QKV_ROPE) ? (uint32_t)a.d_pos[0] : 0u;
+    const size_t kvrow = (a.epi == EPI_QKV_ROPE && a.d_rowbase) ? (size_t)(uint32_t)a.d_rowbase[0] + pos : pos;
+    int smode = SAMPLE_ARGMAX;
+    float spen = 1.0f;
+    if (a.epi == EPI_ARGMAX && a.sampler) {
+        smode = a.sampler->mode;
+        spen = a.sampler->penalty;
+    }
     // Per-group side data (the residual, or the RoPE cos/sin pair) is read
     // before the next group's weights are requested, so waiting for it never
     // waits for the prefetch.
@@ -840,7 +850,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
                         q[a.half_hd] = y1;
                     } else {
                         const uint32_t gk = g - a.q_pairs, h = gk / a.half_hd, i = gk % a.half_hd;
-                        const size_t at = (size_t)pos * a.kv_row + (size_t)h * 2 * a.half_hd + i;
+                        const size_t at = kvrow * a.kv_row + (size_t)h * 2 * a.half_hd + i;
                         if (a.kv_f16) {
                             ((_Float16 *)a.kc)[at] = (_Float16)y0;
                             ((_Float16 *)a.kc)[at + a.half_hd] = (_Float16)y1;
@@ -850,7 +860,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
                         }
                     }
                 } else {
-                    const size_t at = (size_t)pos * a.kv_row + 2 * (size_t)(g - a.q_pairs - a.k_pairs);
+                    const size_t at = kvrow * a.kv_row + 2 * (size_t)(g - a.q_pairs - a.k_pairs);
                     if (a.kv_f16) {
                         ((_Float16 *)a.vc)[at] = (_Float16)r0;
                         ((_Float16 *)a.vc)[at + 1] = (_Float16)r1;
@@ -868,7 +878,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
             if (a.out_f16) ((uint16_t *)a.y)[row] = f2h_bits(s);
             else ((float *)a.y)[row] = s;
             if (a.epi == EPI_ARGMAX) {
-                const uint64_t key = argmax_key(s, row);
+                const uint64_t key = sampler_key(s, row, a.counts, smode, spen);
                 best = key > best ? key : best;
             }
         }
@@ -1346,8 +1356,9 @@ int launch_pair_fmt(janus_ctx *ctx, const GemvArgs &a) {
 namespace janus {
 
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
-                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
-                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma, float eps) {
+                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, const int32_t *d_rowbase,
+                       uint32_t q_pairs, uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma,
+                       float eps) {
     GemvArgs a;
     std::memset(&a, 0, sizeof(a));
     a.gamma = gamma;
@@ -1365,6 +1376,7 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
     a.kv_f16 = kv_f16;
     a.rope = rope;
     a.d_pos = d_pos;
+    a.d_rowbase = d_rowbase;
     a.q_pairs = q_pairs;
     a.k_pairs = k_pairs;
     a.half_hd = half_hd;
@@ -1391,7 +1403,7 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
 }
 
 int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
-                       unsigned long long *best) {
+                       unsigned long long *best, const uint32_t *counts, const SamplerDev *sampler) {
     GemvArgs a;
     std::memset(&a, 0, sizeof(a));
     a.w.qs = w->qs;
@@ -1402,6 +1414,8 @@ int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float
     a.k = w->k;
     a.epi = best ? EPI_ARGMAX : EPI_STORE;
     a.best = best;
+    a.counts = counts;
+    a.sampler = sampler;
     a.gamma = gamma;
     a.eps = eps;
     bool done = false;

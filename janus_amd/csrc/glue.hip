@@ -282,12 +282,22 @@ int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vo
 // Each 1024-thread workgroup scans 32768 logits of one row (8 float4 per
 // thread, all loads in flight together), reduces its keys through LDS and
 // posts one atomicMax: a row's slot takes one device-scope atomic per
-// workgroup (4 for a 128k vocabulary) rather than one per wavefront.
+// workgroup (4 for a 128k vocabulary) rather than one per wavefront. The key
+// is sampler_key under the sampler state (SAMPLE_ARGMAX when null).
 __global__ __launch_bounds__(1024) void argmax_keys_kernel(const float *__restrict__ logits,
-                                                           unsigned long long *best, uint32_t vocab) {
+                                                           unsigned long long *best, uint32_t vocab,
+                                                           const uint32_t *__restrict__ counts,
+                                                           const SamplerDev *__restrict__ sampler) {
     __shared__ uint64_t wbest[16];
     const uint32_t row = blockIdx.y;
     const float *l = logits + (size_t)row * vocab;
+    const uint32_t *cnt = counts ? counts + (size_t)row * vocab : nullptr;
+    int mode = SAMPLE_ARGMAX;
+    float pen = 1.0f;
+    if (sampler) {
+        mode = sampler->mode;
+        pen = sampler->penalty;
+    }
     const uint32_t base = blockIdx.x * 32768u + threadIdx.x * 4u;
     uint64_t key = 0;
     float4 v[8];
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(1024) void argmax_keys_kernel(const float *__restri
     }
     auto take = [&](float x, uint32_t i) {
         if (i < vocab) {
-            const uint64_t k = argmax_key(x, i);
+            const uint64_t k = sampler_key(x, i, cnt, mode, pen);
             key = k > key ? k : key;
         }
     };
@@ -334,28 +344,39 @@ __global__ __launch_bounds__(1024) void argmax_keys_kernel(const float *__restri
 }
 
 int argmax_keys_launch(janus_ctx *ctx, const float *logits, unsigned long long *best, uint32_t vocab,
-                       uint32_t batch) {
+                       uint32_t batch, const uint32_t *counts, const SamplerDev *sampler) {
     hipLaunchKernelGGL(argmax_keys_kernel, dim3((vocab + 32767) / 32768, batch), dim3(1024), 0, ctx->stream, logits,
-                       best, vocab);
+                       best, vocab, counts, sampler);
     JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
 }
 
-// Sequential in context order so repeated ids compound exactly as the host loop.
-__global__ void penalty_kernel(float *logits, uint32_t vocab, const int32_t *__restrict__ ctx_ids, uint32_t n,
-                               float penalty) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    for (uint32_t i = 0; i < n; ++i) {
-        uint32_t t = (uint32_t)ctx_ids[i];
-        if (t < vocab) {
-            float v = logits[t];
-            logits[t] = v > 0.0f ? v / penalty : v * penalty;
-        }
-    }
+// Repetition penalty over a token list (sampler.rs:599-613). Thread i owns
+// list entry i when it is the first occurrence of its id: it counts the
+// id's occurrences and applies that many divides (positive logit) or
+// multiplies (otherwise) in sequence. The sign of a logit never changes
+// under either operation, so the result equals the reference's pass over
+// the list in order; distinct ids touch distinct logits.
+__global__ __launch_bounds__(256) void penalty_kernel(float *logits, uint32_t vocab, const int32_t *__restrict__ ids,
+                                                      uint32_t n, float penalty) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const int32_t t = ids[i];
+    if ((uint32_t)t >= vocab) return;
+    bool first = true;
+    for (uint32_t j = 0; j < i && first; ++j) first = ids[j] != t;
+    if (!first) return;
+    uint32_t c = 1;
+    for (uint32_t j = i + 1; j < n; ++j) c += ids[j] == t ? 1u : 0u;
+    float v = logits[t];
+    for (; c; --c) v = v > 0.0f ? v / penalty : v * penalty;
+    logits[t] = v;
 }
 
 int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t *ids, uint32_t n, float penalty) {
-    hipLaunchKernelGGL(penalty_kernel, dim3(1), dim3(64), 0, ctx->stream, logits, vocab, ids, n, penalty);
+    if (n == 0) return JANUS_OK;
+    hipLaunchKernelGGL(penalty_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, logits, vocab, ids, n,
+                       penalty);
     JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
 }

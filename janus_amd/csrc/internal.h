@@ -7,6 +7,7 @@
 #include <type_traits>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/janus_hip.h"
 
@@ -44,7 +45,24 @@ struct janus_ctx {
     // Small-M GEMM split-K partials; grows on first use.
     void *gemm_ws = nullptr;
     size_t gemm_ws_bytes = 0;
+    // Workspaces replaced by a larger one. A captured graph may still write
+    // them, so they are freed only by janus_destroy.
+    std::vector<void *> retired;
 };
+
+// Greedy sampler state in device memory, read by the argmax kernels, so a
+// captured decode step follows a change without being captured again.
+//  SAMPLE_ARGMAX : last maximal index, no penalty.
+//  SAMPLE_PENALTY: repetition penalty over the generated tokens, then the
+//                  last maximal index (model/sampler.rs:146-209,599-613,784-795).
+//  SAMPLE_WGSL   : the GPU argmax of shaders/argmax.wgsl:26-126, which the
+//                  reference takes when |penalty - 1| < 0.01 (sampler.rs:154-160).
+enum { SAMPLE_ARGMAX = 0, SAMPLE_PENALTY = 1, SAMPLE_WGSL = 2 };
+struct SamplerDev {
+    float penalty;
+    int32_t mode;
+};
+
 
 // HBM layout of an uploaded weight. Rows are the output dimension n.
 //  Q4_0 : qs  = n * nb * 16 bytes (GGML nibble order per block), 16-B aligned
@@ -101,18 +119,20 @@ int need_device(janus_ctx *ctx);
 int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w, void *y, int y_dt,
                   const float *residual);
 // Paired-row M = 1 products: epi 0 = fused QKV with RoPE and KV append (q
-// rotated into y, f32), epi 1 = fused gate/up with SwiGLU into y. x is f16,
-// or, with gamma set, the f32 residual stream RMS-normalised in the kernel.
+// rotated into y, f32; K/V land in cache row rowbase[0] + pos[0], rowbase may
+// be null for 0), epi 1 = fused gate/up with SwiGLU into y. x is f16, or,
+// with gamma set, the f32 residual stream RMS-normalised in the kernel.
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
-                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, uint32_t q_pairs,
-                       uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma = nullptr,
-                       float eps = 0.0f);
+                       void *vc, int kv_f16, const float *rope, const int32_t *d_pos, const int32_t *d_rowbase,
+                       uint32_t q_pairs, uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row,
+                       const float *gamma = nullptr, float eps = 0.0f);
 // M = 1 product of RMSNorm(x, gamma, eps) (x f32) into y (f32). With best
 // set, the outputs are also folded into *best as the running maximum of
-// (order-preserving key << 32 | row): the greedy last-max argmax
-// (model/sampler.rs:784-795); *best must be 0 before the launch.
+// sampler_key (counts: the row's occurrence counts of generated tokens, or
+// null); *best must be 0 before the launch.
 int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
-                       unsigned long long *best);
+                       unsigned long long *best, const uint32_t *counts = nullptr,
+                       const SamplerDev *sampler = nullptr);
 // Row layout of an uploaded weight (bytes of quants, binary16 scales per row).
 size_t weight_qs_row_bytes(int type, uint32_t k);
 size_t weight_sc_row_elems(int type, uint32_t k);
@@ -137,7 +157,8 @@ struct GemmPartials {
 // partials and finishes the step:
 //  gemm_qkv_rope: rows of the fused QKV weight (RoPE pairs of the q heads,
 //    of the k heads, then v) -> q rotated (f32 [rows][q_pairs * 2]), k rotated
-//    and v appended to the cache row m * max_seq + pos[m] (kv_row elements).
+//    and v appended to the cache row rowbase[m] + pos[m] (kv_row elements;
+//    m * max_seq + pos[m] when rowbase is null).
 //  gemm_swiglu: interleaved gate/up rows -> act (binary16 [rows][n / 2]).
 //  gemm_residual_norm: out = resid + product (f32, may alias resid), then
 //    xn = RMSNorm(out) * gamma (binary16), one workgroup per row.
@@ -146,6 +167,7 @@ struct QkvEpilogue {
     void *kc, *vc;
     const float *rope;
     const int32_t *pos;
+    const int32_t *rowbase;   // KV row base per row (null: m * max_seq)
     uint32_t q_pairs, k_pairs, half_hd, kv_row, max_seq;
 };
 int gemm_qkv_rope(janus_ctx *ctx, const void *a16, const janus_weight *w, uint32_t rows, const QkvEpilogue &e,
@@ -167,21 +189,32 @@ int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, voi
 // Attention split sizing shared by the launch and workspace reservation.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
                     int kv_f16, uint32_t *chunk, uint32_t *nw, uint32_t *splits, uint32_t *qh_div);
+// Bytes of split partials a launch of this shape writes (0: no split).
+size_t attention_ws_bytes(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                          uint32_t max_len, int kv_f16);
 int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                       uint32_t max_len, int kv_f16);
-// out is f32, or binary16 when out_f16 is set.
+// out is f32, or binary16 when out_f16 is set. With fixed_ws set the split
+// partials go there (JANUS_E_INVALID_DIM when they need more than
+// fixed_ws_bytes) and nothing is allocated; otherwise into the context's
+// workspace, grown on demand.
 int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
                      uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
-                     float scale, int out_f16 = 0);
+                     float scale, int out_f16 = 0, float *fixed_ws = nullptr, size_t fixed_ws_bytes = 0);
 int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
                  uint32_t batch, float *out);
 int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie);
-// Last-max argmax of each row as a running atomicMax of argmax_key into
+// Greedy choice of each row as a running atomicMax of sampler_key into
 // best[row] (zero before the call; the caller reads and clears it), the
-// rows split over many workgroups.
+// rows split over many workgroups. counts: [batch][vocab] occurrence counts
+// of the generated tokens (read under SAMPLE_PENALTY), or null; sampler
+// null means SAMPLE_ARGMAX.
 int argmax_keys_launch(janus_ctx *ctx, const float *logits, unsigned long long *best, uint32_t vocab,
-                       uint32_t batch);
+                       uint32_t batch, const uint32_t *counts = nullptr, const SamplerDev *sampler = nullptr);
+// Repetition penalty over a token list in list order (sampler.rs:599-613),
+// parallel over distinct ids: each id's occurrences are applied in sequence
+// by one lane.
 int penalty_launch(janus_ctx *ctx, float *logits, uint32_t vocab, const int32_t *ids, uint32_t n, float penalty);
 
 }  // namespace janus
@@ -242,6 +275,38 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     const uint32_t u = __float_as_uint(v);
     const uint32_t k = (v != v) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
     return ((uint64_t)k << 32) | idx;
+}
+
+// Argmax key of logit v at index idx under the sampler state s.
+//  SAMPLE_PENALTY: v first takes the repetition penalty once per occurrence
+//    of idx among the generated tokens (counts[idx]; sampler.rs:599-613:
+//    divide when positive, else multiply). Occurrences of one id are applied
+//    in order and ids do not interact, so this equals the reference's loop
+//    over the context. Then the last-max key.
+//  SAMPLE_WGSL: among equal values the smallest (bitrev8(idx % 256), idx)
+//    wins, and values not above -1e38 (or NaN) count as -1e38 at index 0:
+//    the per-lane strict '>' scan from -1e38 and the strict '>' tree of
+//    shaders/argmax.wgsl:26-126. Index below 2^24.
+__device__ __forceinline__ uint64_t sampler_key(float v, uint32_t idx, const uint32_t *counts, int mode,
+                                                float penalty) {
+    if (mode == SAMPLE_WGSL) {
+        if (!(v > -1e38f)) {
+            v = -1e38f;
+            idx = 0;
+        }
+        const uint32_t u = __float_as_uint(v);
+        const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        const uint32_t pri = (__builtin_bitreverse32(idx & 255u) & 0xff000000u) | idx;
+        return ((uint64_t)k << 32) | (uint32_t)~pri;
+    }
+    if (mode == SAMPLE_PENALTY && counts)
+        for (uint32_t c = counts[idx]; c; --c) v = v > 0.0f ? v / penalty : v * penalty;
+    return argmax_key(v, idx);
+}
+
+// Token index held by a nonzero sampler_key.
+__device__ __forceinline__ uint32_t sampler_key_index(uint64_t key, int mode) {
+    return mode == SAMPLE_WGSL ? (~(uint32_t)key) & 0xffffffu : (uint32_t)key;
 }
 
 // Sum over all 64 lanes of a wavefront; every lane receives the total.

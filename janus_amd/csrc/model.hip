@@ -2,13 +2,25 @@
 //
 // Reference call stack mirrored here (crates/janus-engine/src/):
 //   Model::forward            model/transformer/forward.rs:25-119
+//   Model::forward_batch      model/transformer/forward.rs:141-245
 //   TransformerBlock::forward model/block.rs:190-458 (op order per layer)
 //   Model::generate           model/transformer/generation.rs:129-323
+//   Model::generate_batch     model/transformer/generation.rs:673-870
 //   Sampler::sample (greedy)  model/sampler.rs:146-209, 599-613, 784-795
+//   Sampler::sample_batch     model/sampler.rs:379-428
 // Differences by design: the o-proj and down-proj residual adds are fused
 // into the products' epilogues (same f32 addition), SiLU and the gate*up
-// product are one kernel, K/V may be stored as binary16, and every sequence
-// of a batch carries its own position (the reference shares one, rope.wgsl:64-66).
+// product are one kernel, K/V may be stored as binary16, every sequence of a
+// batch carries its own position (the reference shares one, rope.wgsl:64-66)
+// and its own KV slot (a row-base table), and sampling runs on the device.
+//
+// Decode state lives on the device, one entry per batch row: the token the
+// next step consumes, its position, the KV row base, the prompt still to
+// prefill, the generated tokens, their occurrence counts (the repetition
+// penalty's context) and a done flag. One step (forward, greedy choice,
+// advance) is either enqueued directly or captured once per row count into a
+// HIP graph and replayed; generate and generate_batch both run on replays.
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <string>
@@ -18,6 +30,25 @@
 #include "internal.h"
 
 using namespace janus;
+
+namespace {
+
+// Per-row control block of the device-side decode loop.
+struct RowDev {
+    int32_t prompt_len;   // prompt tokens at prompts[row][0, prompt_len); 0: decode from the first step
+    int32_t max_new;      // the row is done after this many generated tokens
+    int32_t nout;         // generated tokens so far (out[row][0, nout))
+    int32_t done;
+    int32_t eos_mode;     // EOS_* below
+    int32_t pad;
+};
+
+// What a generated 128001 / 128009 (LLAMA3_END_OF_TEXT_ID / LLAMA3_EOT_ID) does.
+enum { EOS_IGNORE = 0, EOS_STOP_DROP = 1, EOS_STOP_KEEP = 2 };
+
+constexpr int kMaxRows = 64;
+
+}  // namespace
 
 struct janus_model {
     janus_ctx *ctx = nullptr;
@@ -44,12 +75,19 @@ struct janus_model {
     bool kv_external = false;
     size_t layer_kv_elems = 0;
     float *rope = nullptr;
-    int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_gen = nullptr;
-    unsigned long long *d_best = nullptr;   // graph decode: folded argmax of the LM head (zero between steps)
-    std::vector<uint32_t> h_pos;   // graph mode: host mirror of device positions
+    // device decode state, max_batch rows
+    int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_rowbase = nullptr;
+    RowDev *d_rows = nullptr;
+    int32_t *d_prompts = nullptr;   // [max_batch][max_seq_len]
+    int32_t *d_out = nullptr;       // [max_batch][max_seq_len]
+    uint32_t *d_counts = nullptr;   // [max_batch][vocab]
+    unsigned long long *d_best = nullptr;   // greedy key per row (zero between steps)
+    SamplerDev *d_sampler = nullptr;
+    SamplerDev h_sampler{1.0f, SAMPLE_ARGMAX};
+    // captured steps, one per row count
+    std::vector<hipGraphExec_t> graphs;
+    std::vector<uint32_t> h_pos;   // graph_run: host mirror of the rows' positions
     uint32_t graph_nseq = 0;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t graph_exec = nullptr;
     hipStream_t cap_stream = nullptr;
 };
 
@@ -66,23 +104,63 @@ int parse_layer_name(const std::string &name, uint32_t *layer, std::string *rest
     return 1;
 }
 
-// End of a graph decode step: advance positions; when the LM head folded the
-// argmax into *best, take the token from it and clear it for the next step.
-__global__ void advance_pos_kernel(int32_t *pos, int32_t *lens, uint32_t n, unsigned long long *best,
-                                   int32_t *tokens) {
-    uint32_t i = threadIdx.x;
-    if (i < n) {
-        pos[i] += 1;
-        lens[i] = pos[i] + 1;
-        if (best) {
-            tokens[i] = (int32_t)(uint32_t)(best[i] & 0xffffffffull);
-            best[i] = 0;
+struct AdvanceArgs {
+    int32_t *pos, *lens, *tokens;
+    RowDev *rows;
+    const int32_t *prompts;
+    int32_t *out;
+    uint32_t *counts;
+    unsigned long long *best;
+    const SamplerDev *sampler;
+    uint32_t n, max_seq, vocab;
+};
+
+// End of a decode step, one lane per row. The step consumed tokens[r] at
+// position pos[r]; the next token is the next prompt token while the prompt
+// lasts, the last prompt token again right after it (the first decode step
+// re-feeds it at position n, generation.rs:176,217), and from then on the
+// greedy choice of this step (best[r]). A chosen token is appended to the
+// row's generated list and counted for the repetition penalty. Done rows
+// keep their state; their attention length drops to one row.
+__global__ void advance_kernel(AdvanceArgs a) {
+    const uint32_t r = threadIdx.x;
+    if (r >= a.n) return;
+    const unsigned long long key = a.best[r];
+    a.best[r] = 0;
+    RowDev c = a.rows[r];
+    if (c.done) return;
+    const int32_t p = a.pos[r];
+    int32_t next;
+    if (p + 1 < c.prompt_len) {
+        next = a.prompts[(size_t)r * a.max_seq + p + 1];
+    } else if (p + 1 == c.prompt_len) {
+        next = a.prompts[(size_t)r * a.max_seq + p];
+    } else {
+        next = (int32_t)sampler_key_index(key, a.sampler->mode);
+        if ((uint32_t)next >= a.vocab) next = 0;
+        const bool eos = next == 128001 || next == 128009;
+        if (!(eos && c.eos_mode == EOS_STOP_DROP)) {
+            if ((uint32_t)c.nout < a.max_seq) a.out[(size_t)r * a.max_seq + c.nout] = next;
+            c.nout += 1;
+            a.counts[(size_t)r * a.vocab + next] += 1;
+        }
+        if ((eos && c.eos_mode != EOS_IGNORE) || c.nout >= c.max_new) c.done = 1;
+    }
+    a.tokens[r] = next;
+    if (!c.done) {
+        if ((uint32_t)p + 1 >= a.max_seq) {
+            c.done = 1;   // no room for another position (generation.rs:200-205)
+        } else {
+            a.pos[r] = p + 1;
+            a.lens[r] = p + 2;
         }
     }
+    if (c.done) a.lens[r] = 1;
+    a.rows[r] = c;
 }
 
 // One decode step over nseq rows whose ids are either host ids or device ids
-// and whose positions / lengths are already in d_pos / d_lens.
+// and whose positions / lengths / row bases are already on the device.
 int forward_rows(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t nseq, uint32_t max_len) {
     janus_ctx *ctx = m->ctx;
     const janus_model_config &c = m->cfg;
@@ -100,14 +178,15 @@ int forward_rows(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, ui
         if ((e = gemm_dispatch(ctx, m->xn, c.act_dtype, L.v, m->v, JANUS_DT_F32, nseq, nullptr))) return e;
         if ((e = rope_launch(ctx, m->q, m->q, m->rope, nseq, c.heads, c.head_dim, 0, m->d_pos))) return e;
         if ((e = rope_launch(ctx, m->k, m->k, m->rope, nseq, c.kv_heads, c.head_dim, 0, m->d_pos))) return e;
-        if ((e = kv_update_launch(ctx, m->k, m->v, kc, vc, c.kv_dtype, nseq, kvd, 0, c.max_seq_len, nullptr,
+        if ((e = kv_update_launch(ctx, m->k, m->v, kc, vc, c.kv_dtype, nseq, kvd, 0, c.max_seq_len, m->d_rowbase,
                                   m->d_pos)))
             return e;
         // attention output in the products' activation dtype
         const bool a16 = c.act_dtype == JANUS_DT_F16;
         void *att = a16 ? m->attn16 : (void *)m->attn;
         if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, att, nseq, c.heads, c.kv_heads, c.head_dim, 0,
-                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), a16)))
+                                  c.max_seq_len, m->d_rowbase, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim),
+                                  a16)))
             return e;
         // o-proj with the residual add fused: h1 = hidden + attn . Wo^T
         if ((e = gemm_dispatch(ctx, att, c.act_dtype, L.o, m->h1, JANUS_DT_F32, nseq, m->hidden))) return e;
@@ -181,7 +260,7 @@ int ensure_fused(janus_model *m) {
 }
 
 // The LM head runs as one LDS-staged GEMV with the final RMSNorm fused in
-// (and optionally the argmax) when its rows fit that kernel.
+// (and optionally the greedy choice) when its rows fit that kernel.
 bool can_fold_head(const janus_model *m) {
     const janus_weight *w = m->lm_head;
     if (w->type != JANUS_DT_F16 || w->k % 8) return false;
@@ -192,9 +271,9 @@ bool can_fold_head(const janus_model *m) {
 // QKV (with the attention RMSNorm in its prologue and RoPE + KV append in its
 // epilogue), attention, o-proj + residual, gate/up (FFN RMSNorm prologue,
 // SwiGLU epilogue), down-proj + residual; the final RMSNorm runs in the LM
-// head's prologue.
+// head's prologue, and with fold_sample the greedy choice in its epilogue.
 int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t max_len,
-                   bool fold_argmax = false) {
+                   bool fold_sample = false) {
     janus_ctx *ctx = m->ctx;
     const janus_model_config &c = m->cfg;
     const uint32_t kvd = c.kv_heads * c.head_dim, half = c.head_dim / 2;
@@ -205,26 +284,25 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
         const janus_model::Layer &L = m->layers[l];
         void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
         void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
-        if ((e = gemv_pair_dispatch(ctx, m->hidden, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, c.heads * half,
-                                    c.kv_heads * half, half, kvd, L.attn_norm, c.rms_eps)))
+        if ((e = gemv_pair_dispatch(ctx, m->hidden, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, m->d_rowbase,
+                                    c.heads * half, c.kv_heads * half, half, kvd, L.attn_norm, c.rms_eps)))
             return e;
         if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, 1, c.heads, c.kv_heads, c.head_dim, 0,
-                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), 1)))
+                                  c.max_seq_len, m->d_rowbase, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim),
+                                  1)))
             return e;
         if ((e = gemm_dispatch(ctx, m->attn16, JANUS_DT_F16, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
-        if ((e = gemv_pair_dispatch(ctx, m->h1, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, 0,
-                                    0, L.ffn_norm, c.rms_eps)))
+        if ((e = gemv_pair_dispatch(ctx, m->h1, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0,
+                                    0, 0, 0, L.ffn_norm, c.rms_eps)))
             return e;
         if ((e = gemm_dispatch(ctx, m->act, JANUS_DT_F16, L.down, m->hidden, JANUS_DT_F32, 1, m->h1))) return e;
     }
     if (can_fold_head(m))
         return gemv_norm_dispatch(ctx, m->hidden, m->out_norm, c.rms_eps, m->lm_head, m->logits,
-                                  fold_argmax ? m->d_best : nullptr);
+                                  fold_sample ? m->d_best : nullptr, m->d_counts, m->d_sampler);
     if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, m->out_norm, 1, c.hidden, c.rms_eps))) return e;
     return gemm_dispatch(ctx, m->xn, JANUS_DT_F16, m->lm_head, m->logits, JANUS_DT_F32, 1, nullptr);
 }
-
-bool can_fold_argmax(const janus_model *m) { return can_fold_head(m); }
 
 bool use_fused1(const janus_model *m, uint32_t nseq) {
     // the fused norms stage x in registers: hidden <= 8192
@@ -267,11 +345,12 @@ int forward_batch(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, u
         const janus_model::Layer &L = m->layers[l];
         void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
         void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
-        const QkvEpilogue qe{m->q, kc, vc, m->rope, m->d_pos, c.heads * half, c.kv_heads * half, half, kvd,
-                             c.max_seq_len};
+        const QkvEpilogue qe{m->q, kc, vc, m->rope, m->d_pos, m->d_rowbase, c.heads * half, c.kv_heads * half, half,
+                             kvd, c.max_seq_len};
         if ((e = gemm_qkv_rope(ctx, m->xn, L.qkv, nseq, qe, kv16))) return e;
         if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, nseq, c.heads, c.kv_heads, c.head_dim, 0,
-                                  c.max_seq_len, nullptr, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim), 1)))
+                                  c.max_seq_len, m->d_rowbase, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim),
+                                  1)))
             return e;
         if ((e = gemm_residual_norm(ctx, m->attn16, L.o, nseq, m->hidden, m->h1, L.ffn_norm, c.rms_eps, m->xn)))
             return e;
@@ -283,40 +362,247 @@ int forward_batch(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, u
 }
 
 int forward_any(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uint32_t nseq, uint32_t max_len,
-                bool fold_argmax) {
-    if (use_fused1(m, nseq)) return forward_fused1(m, h_ids, d_ids, max_len, fold_argmax);
+                bool fold_sample) {
+    if (use_fused1(m, nseq)) return forward_fused1(m, h_ids, d_ids, max_len, fold_sample);
     if (use_fused_batch(m, nseq)) return forward_batch(m, h_ids, d_ids, nseq, max_len);
     return forward_rows(m, h_ids, d_ids, nseq, max_len);
 }
 
-struct Positions {
-    int32_t p[64];
-};
-
-// Positions travel as kernel arguments, so the update is ordered on the
-// stream behind any still-running step that reads the previous values.
-__global__ void set_positions_kernel(Positions pos, int32_t *d_pos, int32_t *d_lens, uint32_t n) {
-    uint32_t i = threadIdx.x;
-    if (i < n) {
-        d_pos[i] = pos.p[i];
-        d_lens[i] = pos.p[i] + 1;
-    }
+// One full decode step over rows 0..nseq-1 from the device state: forward
+// (every row to max_seq_len capacity), greedy choice (folded into the
+// single-sequence LM head, or keyed over the logits), advance.
+int step_launch(janus_model *m, uint32_t nseq) {
+    janus_ctx *ctx = m->ctx;
+    const bool fold = use_fused1(m, nseq) && can_fold_head(m);
+    int e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, fold);
+    if (!e && !fold) e = argmax_keys_launch(ctx, m->logits, m->d_best, m->cfg.vocab, nseq, m->d_counts, m->d_sampler);
+    if (e) return e;
+    AdvanceArgs a;
+    a.pos = m->d_pos;
+    a.lens = m->d_lens;
+    a.tokens = m->d_tokens;
+    a.rows = m->d_rows;
+    a.prompts = m->d_prompts;
+    a.out = m->d_out;
+    a.counts = m->d_counts;
+    a.best = m->d_best;
+    a.sampler = m->d_sampler;
+    a.n = nseq;
+    a.max_seq = m->cfg.max_seq_len;
+    a.vocab = m->cfg.vocab;
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(kMaxRows), 0, ctx->stream, a);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
 }
 
-int upload_positions(janus_model *m, const uint32_t *positions, uint32_t nseq) {
-    Positions p;
-    std::memset(&p, 0, sizeof(p));
-    for (uint32_t i = 0; i < nseq; ++i) p.p[i] = (int32_t)positions[i];
-    hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(64), 0, m->ctx->stream, p, m->d_pos, m->d_lens, nseq);
+struct RowInit {
+    int32_t token[kMaxRows], pos[kMaxRows], rowbase[kMaxRows];
+    RowDev ctl[kMaxRows];
+    uint32_t mask[2];   // rows to set (bit r of mask[r / 32])
+    uint32_t set_ctl;   // also write the control blocks
+};
+
+// Sets the device state of the masked rows from kernel arguments, ordered on
+// the stream behind any step still reading the old values.
+__global__ void set_rows_kernel(RowInit in, int32_t *tokens, int32_t *pos, int32_t *lens, int32_t *rowbase,
+                                RowDev *rows) {
+    const uint32_t r = threadIdx.x;
+    if (r >= kMaxRows || !((in.mask[r / 32] >> (r % 32)) & 1u)) return;
+    tokens[r] = in.token[r];
+    pos[r] = in.pos[r];
+    lens[r] = in.pos[r] + 1;
+    rowbase[r] = in.rowbase[r];
+    if (in.set_ctl) rows[r] = in.ctl[r];
+}
+
+int set_rows(janus_model *m, const RowInit &in) {
+    hipLaunchKernelGGL(set_rows_kernel, dim3(1), dim3(kMaxRows), 0, m->ctx->stream, in, m->d_tokens, m->d_pos,
+                       m->d_lens, m->d_rowbase, m->d_rows);
     JANUS_LAUNCH_CHECK(m->ctx);
     return JANUS_OK;
 }
 
-void free_graph(janus_model *m) {
-    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
-    if (m->graph) hipGraphDestroy(m->graph);
-    m->graph_exec = nullptr;
-    m->graph = nullptr;
+// Validates tokens / positions / slots of an eager step and stores them
+// into rows 0..nseq-1. slots == NULL: row s uses slot s.
+int upload_step(janus_model *m, const uint32_t *tokens, const uint32_t *positions, const uint32_t *slots,
+                uint32_t nseq, uint32_t *max_len) {
+    const janus_model_config &c = m->cfg;
+    RowInit in;
+    std::memset(&in, 0, sizeof(in));
+    uint64_t used = 0;
+    *max_len = 0;
+    for (uint32_t i = 0; i < nseq; ++i) {
+        if (positions[i] >= c.max_seq_len)
+            return fail(m->ctx, JANUS_E_KV_OVERFLOW, "KV cache position " + std::to_string(positions[i]) +
+                                                         " exceeds max_seq_len " + std::to_string(c.max_seq_len));
+        if (tokens && tokens[i] >= c.vocab)
+            return fail(m->ctx, JANUS_E_TOKEN_RANGE, "Token ID " + std::to_string(tokens[i]) + " exceeds vocab size");
+        const uint32_t s = slots ? slots[i] : i;
+        if (s >= c.max_batch)
+            return fail(m->ctx, JANUS_E_INVALID_ARG, "KV slot " + std::to_string(s) + " exceeds max_batch");
+        if ((used >> s) & 1u) return fail(m->ctx, JANUS_E_INVALID_ARG, "KV slot " + std::to_string(s) + " used twice");
+        used |= 1ull << s;
+        in.token[i] = tokens ? (int32_t)tokens[i] : 0;
+        in.pos[i] = (int32_t)positions[i];
+        in.rowbase[i] = (int32_t)(s * c.max_seq_len);
+        in.mask[i / 32] |= 1u << (i % 32);
+        *max_len = positions[i] + 1 > *max_len ? positions[i] + 1 : *max_len;
+    }
+    return set_rows(m, in);
+}
+
+int upload_sampler(janus_model *m) {
+    JANUS_HIP_CHECK(m->ctx, hipMemcpyAsync(m->d_sampler, &m->h_sampler, sizeof(SamplerDev), hipMemcpyHostToDevice,
+                                           m->ctx->stream));
+    return JANUS_OK;
+}
+
+void free_graphs(janus_model *m) {
+    for (auto &g : m->graphs) {
+        if (g) (void)hipGraphExecDestroy(g);
+        g = nullptr;
+    }
+    m->graph_nseq = 0;
+}
+
+// The captured step for nseq rows, captured on first use. Capture follows one
+// eager forward over the same rows (it sets kernel attributes and grows the
+// GEMM workspace outside the capture; it writes the K/V rows the next step
+// writes again with the same values).
+int ensure_graph(janus_model *m, uint32_t nseq) {
+    if (m->graphs[nseq]) return JANUS_OK;
+    janus_ctx *ctx = m->ctx;
+    if (int e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, false)) return e;
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+    // Capture on the model's own stream (the caller's may be the legacy
+    // default stream, which cannot be captured); the graph is launched on the
+    // caller's stream afterwards.
+    if (!m->cap_stream) JANUS_HIP_CHECK(ctx, hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
+    hipStream_t user = ctx->stream;
+    ctx->stream = m->cap_stream;
+    hipError_t be = hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal);
+    if (be != hipSuccess) {
+        ctx->stream = user;
+        return hip_fail(ctx, be, "hipStreamBeginCapture");
+    }
+    int e = step_launch(m, nseq);
+    hipGraph_t g = nullptr;
+    hipError_t ce = hipStreamEndCapture(m->cap_stream, &g);
+    ctx->stream = user;
+    if (e) {
+        if (g) (void)hipGraphDestroy(g);
+        return e;
+    }
+    if (ce != hipSuccess) return hip_fail(ctx, ce, "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) return hip_fail(ctx, ie, "hipGraphInstantiate");
+    m->graphs[nseq] = ge;
+    return JANUS_OK;
+}
+
+int replay(janus_model *m, uint32_t nseq, uint32_t steps) {
+    for (uint32_t s = 0; s < steps; ++s) JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(m->graphs[nseq], m->ctx->stream));
+    return JANUS_OK;
+}
+
+struct Request {
+    const uint32_t *prompt;
+    uint32_t n;
+};
+
+// The device-side generation loop for a list of requests, at most max_batch
+// at a time: a request takes the lowest free row (its KV slot), prefills and
+// decodes on graph replays in chunks, and frees the row when done; the next
+// request is admitted between chunks. Nothing is copied between KV slots.
+int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_tokens, int eos_mode,
+                 uint32_t *out_tokens, uint32_t *n_out) {
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    const uint32_t B = c.max_batch;
+    for (size_t i = 0; i < reqs.size(); ++i) {
+        n_out[i] = 0;
+        if (reqs[i].n == 0) return fail(ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
+        if (reqs[i].n > c.max_seq_len)
+            return fail(ctx, JANUS_E_KV_OVERFLOW, "prompt of " + std::to_string(reqs[i].n) +
+                                                      " tokens exceeds max_seq_len " + std::to_string(c.max_seq_len));
+        for (uint32_t t = 0; t < reqs[i].n; ++t)
+            if (reqs[i].prompt[t] >= c.vocab)
+                return fail(ctx, JANUS_E_TOKEN_RANGE,
+                            "Token ID " + std::to_string(reqs[i].prompt[t]) + " exceeds vocab size");
+    }
+    if (int e = janus_model_validate(m)) return e;
+    if (int e = upload_sampler(m)) return e;
+    std::vector<int> row_req(B, -1);
+    std::vector<RowDev> hrows(B);
+    std::vector<int32_t> hpos(B, 0);
+    std::vector<int32_t> tmp;
+    size_t next_req = 0;
+    for (;;) {
+        // admission: free rows take the next requests
+        RowInit in;
+        std::memset(&in, 0, sizeof(in));
+        in.set_ctl = 1;
+        bool any_new = false;
+        for (uint32_t r = 0; r < B && next_req < reqs.size(); ++r) {
+            if (row_req[r] >= 0) continue;
+            const Request &q = reqs[next_req];
+            row_req[r] = (int)next_req++;
+            tmp.assign(q.prompt, q.prompt + q.n);
+            JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_prompts + (size_t)r * c.max_seq_len, tmp.data(), q.n * 4,
+                                                hipMemcpyHostToDevice, ctx->stream));
+            JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));   // tmp is reused
+            JANUS_HIP_CHECK(ctx, hipMemsetAsync(m->d_counts + (size_t)r * c.vocab, 0, (size_t)c.vocab * 4, ctx->stream));
+            in.token[r] = (int32_t)q.prompt[0];
+            in.pos[r] = 0;
+            in.rowbase[r] = (int32_t)(r * c.max_seq_len);
+            in.ctl[r] = RowDev{(int32_t)q.n, (int32_t)max_tokens, 0, 0, eos_mode, 0};
+            in.mask[r / 32] |= 1u << (r % 32);
+            hrows[r] = in.ctl[r];
+            hpos[r] = 0;
+            any_new = true;
+        }
+        if (any_new)
+            if (int e = set_rows(m, in)) return e;
+        uint32_t nrows = 0;
+        for (uint32_t r = 0; r < B; ++r)
+            if (row_req[r] >= 0) nrows = r + 1;
+        if (nrows == 0) break;
+        // free rows below nrows stay done (frozen) until a request takes them
+        if (int e = ensure_graph(m, nrows)) return e;
+        // steps until the first row can be done without an EOS: its prompt,
+        // its tokens, or its capacity
+        uint32_t k = 16;
+        for (uint32_t r = 0; r < nrows; ++r) {
+            if (row_req[r] < 0 || hrows[r].done) continue;
+            const int64_t left_prompt = hrows[r].prompt_len - hpos[r];   // steps still prefilling
+            int64_t need = (left_prompt > 0 ? left_prompt : 0) + (hrows[r].max_new - hrows[r].nout);
+            const int64_t cap = (int64_t)c.max_seq_len - hpos[r];
+            if (cap < need) need = cap;
+            if (need < 1) need = 1;
+            if ((uint64_t)need < k) k = (uint32_t)need;
+        }
+        if (int e = replay(m, nrows, k)) return e;
+        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(hrows.data(), m->d_rows, nrows * sizeof(RowDev), hipMemcpyDeviceToHost,
+                                            ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(hpos.data(), m->d_pos, nrows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        // retirement: finished rows hand back their tokens and free the row
+        for (uint32_t r = 0; r < nrows; ++r) {
+            if (row_req[r] < 0 || !hrows[r].done) continue;
+            const int i = row_req[r];
+            const uint32_t n = (uint32_t)hrows[r].nout < max_tokens ? (uint32_t)hrows[r].nout : max_tokens;
+            tmp.resize(n ? n : 1);
+            if (n)
+                JANUS_HIP_CHECK(ctx, hipMemcpy(tmp.data(), m->d_out + (size_t)r * c.max_seq_len, n * 4,
+                                               hipMemcpyDeviceToHost));
+            for (uint32_t t = 0; t < n; ++t) out_tokens[(size_t)i * max_tokens + t] = (uint32_t)tmp[t];
+            n_out[i] = n;
+            row_req[r] = -1;
+        }
+    }
+    return JANUS_OK;
 }
 
 }  // namespace
@@ -331,7 +617,10 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
         return fail(ctx, JANUS_E_INVALID_DIM, "model: zero dimension in config");
     if (c.heads % c.kv_heads) return fail(ctx, JANUS_E_INVALID_DIM, "model: heads must be a multiple of kv_heads");
     if (c.head_dim * c.heads != c.hidden) return fail(ctx, JANUS_E_INVALID_DIM, "model: head_dim * heads != hidden");
-    if (c.max_batch == 0 || c.max_batch > 64) return fail(ctx, JANUS_E_INVALID_DIM, "model: max_batch must be 1..64");
+    if (c.max_batch == 0 || c.max_batch > kMaxRows) return fail(ctx, JANUS_E_INVALID_DIM, "model: max_batch must be 1..64");
+    if (c.vocab >= (1u << 24)) return fail(ctx, JANUS_E_INVALID_DIM, "model: vocab must be below 2^24");
+    if ((uint64_t)c.max_batch * c.max_seq_len > (uint64_t)INT_MAX)
+        return fail(ctx, JANUS_E_INVALID_DIM, "model: max_batch * max_seq_len exceeds the row index range");
     if (!is_act_dtype(c.kv_dtype) || !is_act_dtype(c.act_dtype))
         return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "model: kv/act dtype must be F32 or F16");
     if (int e = need_device(ctx)) return e;
@@ -339,7 +628,8 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
     m->ctx = ctx;
     m->cfg = c;
     m->layers.resize(c.layers);
-    const size_t B = c.max_batch, kvd = (size_t)c.kv_heads * c.head_dim;
+    m->graphs.assign(c.max_batch + 1, nullptr);
+    const size_t B = c.max_batch, kvd = (size_t)c.kv_heads * c.head_dim, S = c.max_seq_len;
     auto alloc = [&](void **p, size_t bytes) { return hipMalloc(p, bytes < 256 ? 256 : bytes) == hipSuccess; };
     bool ok = alloc((void **)&m->hidden, B * c.hidden * 4) && alloc((void **)&m->q, B * c.hidden * 4) &&
               alloc((void **)&m->k, B * kvd * 4) && alloc((void **)&m->v, B * kvd * 4) &&
@@ -347,11 +637,24 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
               alloc((void **)&m->gate, B * c.ffn * 4) && alloc((void **)&m->up, B * c.ffn * 4) &&
               alloc((void **)&m->logits, B * c.vocab * 4) && alloc(&m->xn, B * c.hidden * 4) &&
               alloc(&m->act, B * c.ffn * 4) && alloc(&m->attn16, B * c.hidden * 2) &&
-              alloc((void **)&m->rope, (size_t)c.max_seq_len * c.head_dim * 4) &&
-              alloc((void **)&m->d_pos, B * 4) && alloc((void **)&m->d_lens, B * 4) &&
-              alloc((void **)&m->d_tokens, B * 4) && alloc((void **)&m->d_gen, (size_t)c.max_seq_len * 4) &&
-              alloc((void **)&m->d_best, B * 8) && hipMemset(m->d_best, 0, B * 8) == hipSuccess;
-    m->layer_kv_elems = B * c.max_seq_len * kvd;
+              alloc((void **)&m->rope, S * c.head_dim * 4) && alloc((void **)&m->d_pos, kMaxRows * 4) &&
+              alloc((void **)&m->d_lens, kMaxRows * 4) && alloc((void **)&m->d_tokens, kMaxRows * 4) &&
+              alloc((void **)&m->d_rowbase, kMaxRows * 4) && alloc((void **)&m->d_rows, kMaxRows * sizeof(RowDev)) &&
+              alloc((void **)&m->d_prompts, B * S * 4) && alloc((void **)&m->d_out, B * S * 4) &&
+              alloc((void **)&m->d_counts, B * c.vocab * 4) && alloc((void **)&m->d_best, kMaxRows * 8) &&
+              alloc((void **)&m->d_sampler, sizeof(SamplerDev));
+    ok = ok && hipMemset(m->d_best, 0, kMaxRows * 8) == hipSuccess &&
+         hipMemset(m->d_rows, 0, kMaxRows * sizeof(RowDev)) == hipSuccess &&
+         hipMemset(m->d_counts, 0, B * c.vocab * 4) == hipSuccess &&
+         hipMemset(m->d_pos, 0, kMaxRows * 4) == hipSuccess && hipMemset(m->d_tokens, 0, kMaxRows * 4) == hipSuccess &&
+         hipMemcpy(m->d_sampler, &m->h_sampler, sizeof(SamplerDev), hipMemcpyHostToDevice) == hipSuccess;
+    if (ok) {
+        std::vector<int32_t> base(kMaxRows, 0), ones(kMaxRows, 1);
+        for (size_t r = 0; r < B; ++r) base[r] = (int32_t)(r * S);
+        ok = hipMemcpy(m->d_rowbase, base.data(), kMaxRows * 4, hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(m->d_lens, ones.data(), kMaxRows * 4, hipMemcpyHostToDevice) == hipSuccess;
+    }
+    m->layer_kv_elems = B * S * kvd;
     size_t kv_bytes = (size_t)c.layers * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
     ok = ok && alloc(&m->kcache, kv_bytes) && alloc(&m->vcache, kv_bytes);
     if (!ok) {
@@ -362,11 +665,19 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
         janus_model_destroy(m);
         return e;
     }
-    if (int e = attention_reserve(ctx, c.max_batch, c.heads, c.kv_heads, c.head_dim, c.max_seq_len,
-                                  c.kv_dtype == JANUS_DT_F16)) {
-        janus_model_destroy(m);
-        return e;
+    // The attention workspace for every row count at full capacity (captured
+    // steps plan for max_seq_len), so no step ever needs to grow it.
+    size_t need = 0;
+    for (uint32_t b = 1; b <= c.max_batch; ++b) {
+        const size_t n = attention_ws_bytes(ctx, b, c.heads, c.kv_heads, c.head_dim, c.max_seq_len,
+                                            c.kv_dtype == JANUS_DT_F16);
+        need = n > need ? n : need;
     }
+    if (need)
+        if (int e = ensure_attn_ws(ctx, need)) {
+            janus_model_destroy(m);
+            return e;
+        }
     *out = m;
     return JANUS_OK;
 }
@@ -374,7 +685,7 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
 void janus_model_destroy(janus_model *m) {
     if (!m) return;
     hipStreamSynchronize(m->ctx->stream);
-    free_graph(m);
+    free_graphs(m);
     if (m->cap_stream) hipStreamDestroy(m->cap_stream);
     for (auto &L : m->layers) {
         for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down, L.qkv, L.gu}) janus_weight_free(m->ctx, w);
@@ -386,8 +697,9 @@ void janus_model_destroy(janus_model *m) {
     for (void *p : {(void *)m->out_norm, (void *)m->hidden, (void *)m->q, (void *)m->k, (void *)m->v,
                     (void *)m->attn, m->attn16, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
                     m->act, m->kv_external ? nullptr : m->kcache, m->kv_external ? nullptr : m->vcache,
-                    (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens,
-                    (void *)m->d_tokens, (void *)m->d_gen, (void *)m->d_best})
+                    (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens, (void *)m->d_tokens, (void *)m->d_rowbase,
+                    (void *)m->d_rows, (void *)m->d_prompts, (void *)m->d_out, (void *)m->d_counts,
+                    (void *)m->d_best, (void *)m->d_sampler})
         if (p) hipFree(p);
     delete m;
 }
@@ -420,7 +732,8 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
         *dst = w;
         return JANUS_OK;
     };
-    free_graph(m);
+    hipStreamSynchronize(ctx->stream);
+    free_graphs(m);
     m->fused_ready = false;
     m->tiles_ready = false;
     for (auto &L : m->layers) {
@@ -496,7 +809,7 @@ int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_
         return fail(m->ctx, JANUS_E_INVALID_DIM, "set_kv_cache: buffers hold " + std::to_string(bytes_each) +
                                                      " bytes, need " + std::to_string(need));
     JANUS_HIP_CHECK(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    free_graph(m);
+    free_graphs(m);
     if (!m->kv_external) {
         hipFree(m->kcache);
         hipFree(m->vcache);
@@ -511,25 +824,23 @@ int janus_model_reset(janus_model *m) {
     if (!m) return JANUS_E_INVALID_ARG;
     // KVCache::reset only rewinds the position; stale rows are never read
     // because attention reads rows [0, pos + 1).
-    free_graph(m);
+    m->graph_nseq = 0;
     return JANUS_OK;
 }
 
-int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq) {
+int janus_model_forward_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
+                              const uint32_t *slots, uint32_t nseq) {
     if (!m || !tokens || !positions) return JANUS_E_INVALID_ARG;
     if (nseq == 0 || nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "forward: bad batch size");
     if (int e = janus_model_validate(m)) return e;
     uint32_t max_len = 0;
-    for (uint32_t i = 0; i < nseq; ++i) {
-        if (positions[i] >= m->cfg.max_seq_len)
-            return fail(m->ctx, JANUS_E_KV_OVERFLOW, "KV cache position " + std::to_string(positions[i]) +
-                                                         " exceeds max_seq_len " + std::to_string(m->cfg.max_seq_len));
-        if (tokens[i] >= m->cfg.vocab)
-            return fail(m->ctx, JANUS_E_TOKEN_RANGE, "Token ID " + std::to_string(tokens[i]) + " exceeds vocab size");
-        max_len = positions[i] + 1 > max_len ? positions[i] + 1 : max_len;
-    }
-    if (int e = upload_positions(m, positions, nseq)) return e;
+    if (int e = upload_step(m, tokens, positions, slots, nseq, &max_len)) return e;
+    m->graph_nseq = 0;   // the rows no longer hold a graph decode's state
     return forward_any(m, tokens, nullptr, nseq, max_len, false);
+}
+
+int janus_model_forward(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq) {
+    return janus_model_forward_slots(m, tokens, positions, nullptr, nseq);
 }
 
 const float *janus_model_logits(const janus_model *m) { return m ? m->logits : nullptr; }
@@ -541,7 +852,20 @@ void *janus_model_kv_cache(const janus_model *m, int which) {
 
 int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq) {
     if (!m || !h_out) return JANUS_E_INVALID_ARG;
+    if (nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "read_logits: more rows than max_batch");
     return janus_d2h(m->ctx, h_out, m->logits, (size_t)nseq * m->cfg.vocab * 4);
+}
+
+int janus_model_set_sampler(janus_model *m, int mode, float penalty) {
+    if (!m) return JANUS_E_INVALID_ARG;
+    if (mode != JANUS_SAMPLER_ARGMAX && mode != JANUS_SAMPLER_PENALTY && mode != JANUS_SAMPLER_WGSL)
+        return fail(m->ctx, JANUS_E_INVALID_ARG, "set_sampler: unknown mode");
+    if (!(penalty > 0.0f) || !std::isfinite(penalty))
+        return fail(m->ctx, JANUS_E_INVALID_ARG, "set_sampler: penalty must be positive and finite");
+    m->h_sampler.mode = mode == JANUS_SAMPLER_PENALTY ? SAMPLE_PENALTY : mode == JANUS_SAMPLER_WGSL ? SAMPLE_WGSL
+                                                                                                  : SAMPLE_ARGMAX;
+    m->h_sampler.penalty = penalty;
+    return upload_sampler(m);
 }
 
 int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
@@ -549,104 +873,104 @@ int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prom
     if (!m || !prompt || !out_tokens || !n_out) return JANUS_E_INVALID_ARG;
     *n_out = 0;
     if (n_prompt == 0) return fail(m->ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
-    janus_ctx *ctx = m->ctx;
-    // prefill: one forward per prompt token (generation.rs:161-173)
-    uint32_t pos = 0;
-    for (uint32_t i = 0; i < n_prompt; ++i, ++pos)
-        if (int e = janus_model_forward(m, &prompt[i], &pos, 1)) return e;
-    uint32_t last = prompt[n_prompt - 1];
-    std::vector<int32_t> generated;
-    int32_t *d_choice = m->d_tokens;
-    for (uint32_t step = 0; step < max_tokens; ++step) {
-        if (pos >= m->cfg.max_seq_len) break;
-        // the first decode step re-feeds the last prompt token at position n (generation.rs:176,217)
-        if (int e = janus_model_forward(m, &last, &pos, 1)) return e;
-        // sample: penalty over the generated tokens, then the last-max argmax
-        if (!generated.empty()) {
-            JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_gen, generated.data(), generated.size() * 4,
-                                                hipMemcpyHostToDevice, ctx->stream));
-            if (int e = penalty_launch(ctx, m->logits, m->cfg.vocab, m->d_gen, (uint32_t)generated.size(), penalty))
-                return e;
-        }
-        if (int e = argmax_launch(ctx, m->logits, d_choice, m->cfg.vocab, 1, JANUS_TIE_LAST)) return e;
-        int32_t next = 0;
-        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&next, d_choice, 4, hipMemcpyDeviceToHost, ctx->stream));
-        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-        out_tokens[(*n_out)++] = (uint32_t)next;
-        if (next == 128001 || next == 128009) break;   // LLAMA3_END_OF_TEXT_ID / LLAMA3_EOT_ID
-        generated.push_back(next);
-        last = (uint32_t)next;
-        ++pos;
+    if (!(penalty > 0.0f) || !std::isfinite(penalty))
+        return fail(m->ctx, JANUS_E_INVALID_ARG, "generate: penalty must be positive and finite");
+    // Sampler::sample: with the penalty within 0.01 of 1 the reference takes
+    // the GPU argmax (its tie rule, no penalty); otherwise the penalty and the
+    // last-max argmax (sampler.rs:154-160, 188-206).
+    m->h_sampler.mode = std::fabs(penalty - 1.0f) < 0.01f ? SAMPLE_WGSL : SAMPLE_PENALTY;
+    m->h_sampler.penalty = penalty;
+    if (max_tokens == 0) {
+        // prefill only (generation.rs:161-173), then a loop of zero steps
+        for (uint32_t i = 0; i < n_prompt; ++i)
+            if (int e = janus_model_forward(m, &prompt[i], &i, 1)) return e;
+        return upload_sampler(m);
     }
+    std::vector<Request> reqs{Request{prompt, n_prompt}};
+    return run_requests(m, reqs, max_tokens, EOS_STOP_DROP, out_tokens, n_out);
+}
+
+int janus_model_generate_batch(janus_model *m, const uint32_t *prompts, const uint32_t *prompt_lens, uint32_t nreq,
+                               uint32_t max_tokens, float penalty, uint32_t *out_tokens, uint32_t *n_out) {
+    if (!m || (nreq && (!prompts || !prompt_lens || !out_tokens || !n_out))) return JANUS_E_INVALID_ARG;
+    if (nreq == 0 || max_tokens == 0) {
+        for (uint32_t i = 0; i < nreq; ++i) n_out[i] = 0;
+        return JANUS_OK;
+    }
+    if (!(penalty > 0.0f) || !std::isfinite(penalty))
+        return fail(m->ctx, JANUS_E_INVALID_ARG, "generate_batch: penalty must be positive and finite");
+    // Sampler::sample_batch applies the penalty and the last-max argmax to
+    // every sequence (sampler.rs:379-428).
+    m->h_sampler.mode = SAMPLE_PENALTY;
+    m->h_sampler.penalty = penalty;
+    std::vector<Request> reqs(nreq);
+    size_t off = 0;
+    for (uint32_t i = 0; i < nreq; ++i) {
+        reqs[i] = Request{prompts + off, prompt_lens[i]};
+        off += prompt_lens[i];
+    }
+    return run_requests(m, reqs, max_tokens, EOS_STOP_KEEP, out_tokens, n_out);
+}
+
+int janus_model_graph_begin_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
+                                  const uint32_t *slots, uint32_t nseq) {
+    if (!m || !tokens || !positions) return JANUS_E_INVALID_ARG;
+    if (nseq == 0 || nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "graph: bad batch size");
+    janus_ctx *ctx = m->ctx;
+    if (int e = janus_model_validate(m)) return e;
+    uint32_t max_len = 0;
+    if (int e = upload_step(m, tokens, positions, slots, nseq, &max_len)) return e;
+    // plain decode rows: no prompt, no stop, a fresh penalty context
+    RowInit in;
+    std::memset(&in, 0, sizeof(in));
+    in.set_ctl = 1;
+    for (uint32_t i = 0; i < nseq; ++i) {
+        in.token[i] = (int32_t)tokens[i];
+        in.pos[i] = (int32_t)positions[i];
+        in.rowbase[i] = (int32_t)((slots ? slots[i] : i) * m->cfg.max_seq_len);
+        in.ctl[i] = RowDev{0, INT_MAX, 0, 0, EOS_IGNORE, 0};
+        in.mask[i / 32] |= 1u << (i % 32);
+    }
+    if (int e = set_rows(m, in)) return e;
+    JANUS_HIP_CHECK(ctx, hipMemsetAsync(m->d_counts, 0, (size_t)nseq * m->cfg.vocab * 4, ctx->stream));
+    if (int e = upload_sampler(m)) return e;
+    if (int e = ensure_graph(m, nseq)) return e;
+    m->h_pos.assign(positions, positions + nseq);
+    m->graph_nseq = nseq;
     return JANUS_OK;
 }
 
 int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq) {
-    if (!m || !tokens || !positions) return JANUS_E_INVALID_ARG;
-    if (nseq == 0 || nseq > m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_DIM, "graph: bad batch size");
-    janus_ctx *ctx = m->ctx;
-    // Eager step first: checks arguments, sets kernel attributes and grows
-    // workspaces outside of capture. It writes the same K/V rows the first
-    // replay rewrites.
-    if (int e = janus_model_forward(m, tokens, positions, nseq)) return e;
-    std::vector<int32_t> ids(tokens, tokens + nseq);
-    JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_tokens, ids.data(), nseq * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (int e = upload_positions(m, positions, nseq)) return e;
-    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-    m->h_pos.assign(positions, positions + nseq);
-    m->graph_nseq = nseq;
-    free_graph(m);
-    // Capture on the model's own stream (the caller's may be the legacy
-    // default stream, which cannot be captured); the graph is launched on the
-    // caller's stream afterwards.
-    if (!m->cap_stream) JANUS_HIP_CHECK(ctx, hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
-    hipStream_t user = ctx->stream;
-    ctx->stream = m->cap_stream;
-    int e = JANUS_OK;
-    hipError_t be = hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal);
-    if (be != hipSuccess) {
-        ctx->stream = user;
-        return hip_fail(ctx, be, "hipStreamBeginCapture");
-    }
-    // the greedy token: folded into the single-sequence LM head, a keyed
-    // atomicMax over the logits of a batch, or the plain argmax kernel
-    const bool fold = use_fused1(m, nseq) && can_fold_argmax(m);
-    const bool keys = !fold && nseq > 1;
-    e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, fold);
-    if (!e && keys) e = argmax_keys_launch(ctx, m->logits, m->d_best, m->cfg.vocab, nseq);
-    else if (!e && !fold) e = argmax_launch(ctx, m->logits, m->d_tokens, m->cfg.vocab, nseq, JANUS_TIE_LAST);
-    if (!e) {
-        hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, ctx->stream, m->d_pos, m->d_lens, nseq,
-                           (fold || keys) ? m->d_best : nullptr, m->d_tokens);
-        if (hipGetLastError() != hipSuccess) e = JANUS_E_HIP;
-    }
-    hipGraph_t g = nullptr;
-    hipError_t ce = hipStreamEndCapture(m->cap_stream, &g);
-    ctx->stream = user;
-    if (e) {
-        if (g) hipGraphDestroy(g);
-        return e;
-    }
-    if (ce != hipSuccess) return hip_fail(ctx, ce, "hipStreamEndCapture");
-    m->graph = g;
-    JANUS_HIP_CHECK(ctx, hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0));
-    return JANUS_OK;
+    return janus_model_graph_begin_slots(m, tokens, positions, nullptr, nseq);
 }
 
 int janus_model_graph_run(janus_model *m, uint32_t steps) {
     if (!m) return JANUS_E_INVALID_ARG;
-    if (!m->graph_exec) return fail(m->ctx, JANUS_E_INVALID_ARG, "graph: call janus_model_graph_begin first");
-    for (uint32_t i = 0; i < m->graph_nseq; ++i)
+    const uint32_t n = m->graph_nseq;
+    if (!n || !m->graphs[n]) return fail(m->ctx, JANUS_E_INVALID_ARG, "graph: call janus_model_graph_begin first");
+    for (uint32_t i = 0; i < n; ++i)
         if (m->h_pos[i] + steps > m->cfg.max_seq_len)
             return fail(m->ctx, JANUS_E_KV_OVERFLOW, "graph: steps would exceed max_seq_len");
-    for (uint32_t s = 0; s < steps; ++s) JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(m->graph_exec, m->ctx->stream));
+    if (int e = replay(m, n, steps)) return e;
     for (auto &p : m->h_pos) p += steps;
     return JANUS_OK;
 }
 
 int janus_model_graph_read_tokens(janus_model *m, uint32_t *h_tokens, uint32_t nseq) {
-    if (!m || !h_tokens || nseq > m->graph_nseq) return JANUS_E_INVALID_ARG;
+    if (!m || !h_tokens || nseq > m->cfg.max_batch) return JANUS_E_INVALID_ARG;
     return janus_d2h(m->ctx, h_tokens, m->d_tokens, (size_t)nseq * 4);
+}
+
+int janus_model_read_generated(janus_model *m, uint32_t row, uint32_t *h_tokens, uint32_t cap, uint32_t *n) {
+    if (!m || !n || (cap && !h_tokens)) return JANUS_E_INVALID_ARG;
+    if (row >= m->cfg.max_batch) return fail(m->ctx, JANUS_E_INVALID_ARG, "read_generated: row out of range");
+    RowDev c;
+    if (int e = janus_d2h(m->ctx, &c, m->d_rows + row, sizeof(RowDev))) return e;
+    uint32_t total = (uint32_t)c.nout < m->cfg.max_seq_len ? (uint32_t)c.nout : m->cfg.max_seq_len;
+    *n = total;
+    const uint32_t take = total < cap ? total : cap;
+    if (take) return janus_d2h(m->ctx, h_tokens, m->d_out + (size_t)row * m->cfg.max_seq_len, (size_t)take * 4);
+    return JANUS_OK;
 }
 
 }  // extern "C"

@@ -131,11 +131,11 @@ int janus_kv_update(janus_ctx *ctx, const float *k_new, const float *v_new, void
                             max_seq_len, d_row_base, d_positions);
 }
 
-int janus_attention(janus_ctx *ctx, const float *q, const void *k_cache, const void *v_cache, int kv_dt, float *out,
-                    uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
-                    uint32_t max_seq_len, const int32_t *d_row_base, const int32_t *d_seq_lens,
-                    uint32_t max_len_hint, float scale) {
-    if (check_ctx(ctx)) return JANUS_E_INVALID_ARG;
+namespace {
+// Host checks shared by the two attention entry points (ops/attention.rs:78-235).
+int attention_args(janus_ctx *ctx, const float *q, const void *k_cache, const void *v_cache, int kv_dt,
+                   const float *out, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
+                   uint32_t max_seq_len, const int32_t *d_seq_lens) {
     if (!q || !k_cache || !v_cache || !out) return fail(ctx, JANUS_E_INVALID_ARG, "attention: null buffer");
     if (!is_act_dtype(kv_dt)) return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "attention: kv dtype must be F32 or F16");
     if (kv_heads == 0 || heads == 0 || heads % kv_heads)
@@ -143,6 +143,18 @@ int janus_attention(janus_ctx *ctx, const float *q, const void *k_cache, const v
     if (hd != 64 && hd != 128) return fail(ctx, JANUS_E_INVALID_DIM, "attention: head_dim must be 64 or 128");
     if (!d_seq_lens && seq_len > max_seq_len)
         return fail(ctx, JANUS_E_KV_OVERFLOW, "attention: seq_len exceeds max_seq_len");
+    return JANUS_OK;
+}
+}  // namespace
+
+int janus_attention(janus_ctx *ctx, const float *q, const void *k_cache, const void *v_cache, int kv_dt, float *out,
+                    uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
+                    uint32_t max_seq_len, const int32_t *d_row_base, const int32_t *d_seq_lens,
+                    uint32_t max_len_hint, float scale) {
+    if (check_ctx(ctx)) return JANUS_E_INVALID_ARG;
+    if (int e = attention_args(ctx, q, k_cache, v_cache, kv_dt, out, heads, kv_heads, hd, seq_len, max_seq_len,
+                               d_seq_lens))
+        return e;
     if (batch == 0) return JANUS_OK;
     if (int e = need_device(ctx)) return e;
     uint32_t max_len = d_seq_lens ? (max_len_hint ? max_len_hint : max_seq_len) : seq_len;

@@ -24,30 +24,44 @@ int hip_fail(janus_ctx *ctx, hipError_t e, const char *what) {
     return fail(ctx, code, m);
 }
 
-int ensure_attn_ws(janus_ctx *ctx, size_t bytes) {
-    if (ctx->attn_ws_bytes >= bytes) return JANUS_OK;
-    if (ctx->attn_ws) {
-        JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-        JANUS_HIP_CHECK(ctx, hipFree(ctx->attn_ws));
-        ctx->attn_ws = nullptr;
-        ctx->attn_ws_bytes = 0;
+namespace {
+
+// Grows a context workspace to at least `bytes`. The old buffer is retired,
+// not freed: a HIP graph captured earlier may still write it, so it lives
+// until janus_destroy. Growth at least doubles the size, which bounds the
+// retired memory by the final size. Growing while the stream is being
+// captured is refused: the capture would record the new buffer, but
+// allocating inside a capture is not allowed, so the caller must reserve
+// first.
+int grow_workspace(janus_ctx *ctx, void **buf, size_t *have, size_t bytes, size_t floor_bytes, const char *what) {
+    if (*have >= bytes) return JANUS_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(ctx, JANUS_E_INVALID_ARG, std::string(what) + " workspace must grow to " + std::to_string(bytes) +
+                                                  " bytes during graph capture; reserve it before capturing");
+    size_t sz = bytes < floor_bytes ? floor_bytes : bytes;
+    if (*buf && sz < 2 * *have) sz = 2 * *have;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess && sz > bytes && bytes >= floor_bytes) {
+        sz = bytes;   // the doubling failed; the exact size may still fit
+        e = hipMalloc(&p, sz);
     }
-    size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
-    JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->attn_ws, sz));
-    ctx->attn_ws_bytes = sz;
+    if (e != hipSuccess) return hip_fail(ctx, e, what);
+    if (*buf) ctx->retired.push_back(*buf);
+    *buf = p;
+    *have = sz;
     return JANUS_OK;
 }
 
+}  // namespace
+
+int ensure_attn_ws(janus_ctx *ctx, size_t bytes) {
+    return grow_workspace(ctx, &ctx->attn_ws, &ctx->attn_ws_bytes, bytes, 1u << 20, "hipMalloc(attention workspace)");
+}
+
 int ensure_gemm_ws(janus_ctx *ctx, size_t bytes) {
-    if (ctx->gemm_ws_bytes >= bytes) return JANUS_OK;
-    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->gemm_ws) JANUS_HIP_CHECK(ctx, hipFree(ctx->gemm_ws));
-    ctx->gemm_ws = nullptr;
-    ctx->gemm_ws_bytes = 0;
-    size_t sz = bytes < (4u << 20) ? (4u << 20) : bytes;
-    JANUS_HIP_CHECK(ctx, hipMalloc(&ctx->gemm_ws, sz));
-    ctx->gemm_ws_bytes = sz;
-    return JANUS_OK;
+    return grow_workspace(ctx, &ctx->gemm_ws, &ctx->gemm_ws_bytes, bytes, 4u << 20, "hipMalloc(gemm workspace)");
 }
 
 int need_device(janus_ctx *ctx) {
@@ -323,6 +337,7 @@ void janus_destroy(janus_ctx *ctx) {
     if (ctx->stream && ctx->stream != ctx->own_stream) hipStreamSynchronize(ctx->stream);
     if (ctx->attn_ws) hipFree(ctx->attn_ws);
     if (ctx->gemm_ws) hipFree(ctx->gemm_ws);
+    for (void *p : ctx->retired) hipFree(p);
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
@@ -337,6 +352,13 @@ int janus_set_stream(janus_ctx *ctx, void *s) {
 }
 
 void *janus_get_stream(janus_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int janus_workspace_bytes(const janus_ctx *ctx, size_t *attn_bytes, size_t *gemm_bytes) {
+    if (!ctx) return JANUS_E_INVALID_ARG;
+    if (attn_bytes) *attn_bytes = ctx->attn_ws_bytes;
+    if (gemm_bytes) *gemm_bytes = ctx->gemm_ws_bytes;
+    return JANUS_OK;
+}
 
 int janus_sync(janus_ctx *ctx) {
     if (!ctx) return JANUS_E_INVALID_ARG;

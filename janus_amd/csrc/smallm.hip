@@ -1014,8 +1014,8 @@ __device__ __forceinline__ jf2 sum_pair(const GemmPartials &p, uint32_t m, uint3
 
 // Fused-QKV rows (RoPE pairs of q heads, of k heads, then v in order): rotate
 // q into q_out [rows][heads * hd] (f32) and k, append k and v to the cache row
-// m * max_seq + pos[m] (the rotation of rope.wgsl:71-72, the row layout of
-// kv_update_kernel).
+// rowbase[m] + pos[m] (m * max_seq + pos[m] without a table; the rotation of
+// rope.wgsl:71-72, the row layout of kv_update_kernel).
 template <typename KV>
 __global__ __launch_bounds__(256) void epi_qkv_rope_kernel(GemmPartials p, QkvEpilogue e, uint32_t rows) {
     const uint32_t pairs = e.q_pairs + e.k_pairs + e.kv_row / 2;
@@ -1025,7 +1025,7 @@ __global__ __launch_bounds__(256) void epi_qkv_rope_kernel(GemmPartials p, QkvEp
     const uint32_t pos = (uint32_t)e.pos[m];
     if (pos >= e.max_seq) return;   // host checks keep positions in range; never index past the tables
     const jf2 r = sum_pair(p, m, 2 * g);
-    const size_t row = (size_t)m * e.max_seq + pos;
+    const size_t row = (e.rowbase ? (size_t)(uint32_t)e.rowbase[m] : (size_t)m * e.max_seq) + pos;
     if (g < e.q_pairs + e.k_pairs) {
         const bool isq = g < e.q_pairs;
         const uint32_t gg = isq ? g : g - e.q_pairs, h = gg / e.half_hd, i = gg % e.half_hd;

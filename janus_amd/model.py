@@ -76,10 +76,17 @@ class Model:
         except Exception:
             pass
 
-    def forward(self, tokens: Sequence[int], positions: Sequence[int]) -> None:
+    def forward(self, tokens: Sequence[int], positions: Sequence[int], slots: Sequence[int] | None = None) -> None:
+        """One decode step (Model::forward / forward_batch); sequence s uses KV
+        slot slots[s] (default s)."""
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
         p = np.ascontiguousarray(np.asarray(positions, dtype=np.uint32))
-        self._check(self.lib.janus_model_forward(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+        if slots is None:
+            self._check(self.lib.janus_model_forward(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+        else:
+            s = np.ascontiguousarray(np.asarray(slots, dtype=np.uint32))
+            self._check(self.lib.janus_model_forward_slots(self.handle, t.ctypes.data, p.ctypes.data,
+                                                           s.ctypes.data, len(t)))
 
     def logits(self, nseq: int = 1) -> np.ndarray:
         out = np.empty((nseq, self.spec.vocab), dtype=np.float32)
@@ -97,10 +104,38 @@ class Model:
                                                   repetition_penalty, out.ctypes.data, C.byref(n)))
         return out[: n.value].tolist()
 
-    def graph_begin(self, tokens: Sequence[int], positions: Sequence[int]) -> None:
+    def generate_batch(self, prompts: Sequence[Sequence[int]], max_tokens: int,
+                       repetition_penalty: float = 1.15) -> list[list[int]]:
+        """Model::generate_batch with continuous batching (include/janus_model.h)."""
+        lens = np.ascontiguousarray(np.asarray([len(p) for p in prompts], dtype=np.uint32))
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts])
+                                    if len(prompts) else np.zeros(1, np.uint32))
+        out = np.zeros((max(1, len(prompts)), max(1, max_tokens)), dtype=np.uint32)
+        n = np.zeros(max(1, len(prompts)), dtype=np.uint32)
+        self._check(self.lib.janus_model_generate_batch(self.handle, flat.ctypes.data, lens.ctypes.data,
+                                                        len(prompts), max_tokens, repetition_penalty,
+                                                        out.ctypes.data, n.ctypes.data))
+        return [out[i, : n[i]].tolist() for i in range(len(prompts))]
+
+    def set_sampler(self, mode: int, repetition_penalty: float = 1.0) -> None:
+        self._check(self.lib.janus_model_set_sampler(self.handle, mode, repetition_penalty))
+
+    def graph_begin(self, tokens: Sequence[int], positions: Sequence[int], slots: Sequence[int] | None = None) -> None:
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
         p = np.ascontiguousarray(np.asarray(positions, dtype=np.uint32))
-        self._check(self.lib.janus_model_graph_begin(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+        if slots is None:
+            self._check(self.lib.janus_model_graph_begin(self.handle, t.ctypes.data, p.ctypes.data, len(t)))
+        else:
+            s = np.ascontiguousarray(np.asarray(slots, dtype=np.uint32))
+            self._check(self.lib.janus_model_graph_begin_slots(self.handle, t.ctypes.data, p.ctypes.data,
+                                                               s.ctypes.data, len(t)))
+
+    def generated(self, row: int = 0, cap: int = 1 << 16) -> list[int]:
+        """Tokens generated by batch row `row` since its graph_begin or admission."""
+        out = np.zeros(max(1, cap), dtype=np.uint32)
+        n = C.c_uint32()
+        self._check(self.lib.janus_model_read_generated(self.handle, row, out.ctypes.data, cap, C.byref(n)))
+        return out[: min(n.value, cap)].tolist()
 
     def graph_run(self, steps: int) -> None:
         self._check(self.lib.janus_model_graph_run(self.handle, steps))

@@ -63,6 +63,12 @@ class ComputeEngine:
     def sync(self) -> None:
         check(self.lib.janus_sync(self.ctx), self.ctx)
 
+    def workspace_bytes(self) -> tuple[int, int]:
+        """(attention, small-M GEMM) workspace sizes of the context."""
+        a, g = C.c_size_t(), C.c_size_t()
+        check(self.lib.janus_workspace_bytes(self.ctx, C.byref(a), C.byref(g)), self.ctx)
+        return a.value, g.value
+
     def close(self) -> None:
         if self.ctx:
             self.lib.janus_destroy(self.ctx)

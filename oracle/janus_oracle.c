@@ -232,7 +232,10 @@ void jo_dequant_q6_k(const uint8_t *blocks, size_t nblocks, int ref_order, float
 void jo_gemv_q8_0(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k)
 {
     uint32_t nb = k / 32;
-    for (uint32_t r = 0; r < n; ++r) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+    for (long long r = 0; r < (long long)n; ++r) {
         float row = 0.0f;
         for (uint32_t b = 0; b < nb; ++b) {
             const uint8_t *blk = w + ((size_t)r * nb + b) * 34;
@@ -268,7 +271,10 @@ static float q4_0_row(const uint8_t *row_blocks, const float *x, uint32_t nb)
 void jo_gemv_q4_0(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k)
 {
     uint32_t nb = k / 32;
-    for (uint32_t r = 0; r < n; ++r) y[r] = q4_0_row(w + (size_t)r * nb * 18, x, nb);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+    for (long long r = 0; r < (long long)n; ++r) y[r] = q4_0_row(w + (size_t)r * nb * 18, x, nb);
 }
 
 void jo_gemv_q4_0_mt(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k)
@@ -293,8 +299,11 @@ int jo_num_threads(void)
 void jo_gemv_q5_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k, int ftz)
 {
     uint32_t nb = k / 256;
-    float wv[256];
-    for (uint32_t r = 0; r < n; ++r) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+    for (long long r = 0; r < (long long)n; ++r) {
+        float wv[256];
         float row = 0.0f;
         for (uint32_t b = 0; b < nb; ++b) {
             q5k_block(w + ((size_t)r * nb + b) * 176, ftz, wv);
@@ -314,7 +323,10 @@ void jo_gemv_q5_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32
 void jo_gemv_q4_k(const uint8_t *w, const float *x, float *y, uint32_t n, uint32_t k, int ftz)
 {
     uint32_t nb = k / 256;
-    for (uint32_t r = 0; r < n; ++r) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+    for (long long r = 0; r < (long long)n; ++r) {
         float row = 0.0f;
         for (uint32_t b = 0; b < nb; ++b) {
             const uint8_t *blk = w + ((size_t)r * nb + b) * 144;
@@ -348,7 +360,10 @@ void jo_gemm_f16(const float *a, const uint16_t *b, float *c, uint32_t batch,
 {
     for (uint32_t bi = 0; bi < batch; ++bi)
         for (uint32_t i = 0; i < m; ++i)
-            for (uint32_t j = 0; j < n; ++j) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+            for (long long j = 0; j < (long long)n; ++j) {
                 const float *arow = a + ((size_t)bi * m + i) * k;
                 const uint16_t *brow = b + (size_t)j * k;
                 float s = 0.0f;
@@ -359,7 +374,10 @@ void jo_gemm_f16(const float *a, const uint16_t *b, float *c, uint32_t batch,
 
 void jo_gemv_f64(const float *w, const float *x, double *y, uint32_t n, uint32_t k)
 {
-    for (uint32_t r = 0; r < n; ++r) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if ((uint64_t)n * k > (1u << 18))
+#endif
+    for (long long r = 0; r < (long long)n; ++r) {
         double s = 0.0;
         for (uint32_t i = 0; i < k; ++i) s += (double)w[(size_t)r * k + i] * (double)x[i];
         y[r] = s;

@@ -235,9 +235,15 @@ def argmax_wgsl(logits) -> int:
     return int(lib().jo_argmax_wgsl(l, l.size))
 
 
-def greedy_sample(logits, context, penalty: float = 1.15) -> int:
-    """Sampler::sample with temperature 0 (model/sampler.rs:146-209)."""
+def greedy_sample(logits, context, penalty: float = 1.15, batch: bool = False) -> int:
+    """Sampler::sample with temperature 0 (model/sampler.rs:146-209): with
+    |penalty - 1| < 0.01 the GPU argmax of argmax.wgsl (no penalty, its tie
+    rule, :154-160), otherwise the penalty over the context and the last-max
+    argmax. batch=True is Sampler::sample_batch (:379-428), which always
+    applies the penalty and the last-max argmax."""
     l = _f32(logits).copy()
+    if not batch and abs(np.float32(penalty) - np.float32(1.0)) < np.float32(0.01):
+        return argmax_wgsl(l)
     if np.isnan(l).any():
         raise FloatingPointError("NaN logits")
     ctx = np.ascontiguousarray(np.asarray(context, dtype=np.uint32))
@@ -307,7 +313,16 @@ class OracleModel:
         xn = rmsnorm(x, self._vec("output_norm.weight"), s.rms_eps)
         return self._mm("output.weight", xn)
 
-    def generate(self, prompt, max_tokens: int, penalty: float = 1.15, return_logits: bool = False):
+    def generate(self, prompt, max_tokens: int, penalty: float = 1.15, return_logits: bool = False,
+                 batch_rules: bool = False):
+        """Model::generate (generation.rs:129-323): prefill, re-feed the last
+        prompt token at position n, then sample until max_tokens, max_seq_len
+        or 128001/128009, which is not pushed (:241-260).
+
+        batch_rules=True follows one sequence of Model::generate_batch
+        (generation.rs:765-833) as the build's continuous batching runs it:
+        Sampler::sample_batch's rules, and the stop token is pushed before the
+        check."""
         self.reset()
         pos = 0
         for tok in prompt:
@@ -320,9 +335,10 @@ class OracleModel:
                 break
             logits = self.forward(last, pos)
             all_logits.append(logits)
-            nxt = greedy_sample(logits, generated, penalty)
+            nxt = greedy_sample(logits, generated, penalty, batch=batch_rules)
             if nxt in (128001, 128009):
-                generated.append(nxt)
+                if batch_rules:
+                    generated.append(nxt)
                 break
             generated.append(nxt)
             last = nxt

@@ -1,0 +1,159 @@
+"""GPU parity at the benchmark configurations' own shapes.
+
+- Config 3 (Llama-2-7B architecture, Q4_K, MHA 32 heads x 128): a 2-layer
+  model at hidden 4096 / FFN 11008 / vocab 32000 on the fused binary16 path
+  against the oracle at every step (logits within 2e-3, greedy tokens
+  identical), and the full 32-layer model after a 512-token prefill: captured
+  decode steps == eager decode steps.
+- Config 4 (attention microbench): its seeded lengths U[128, 8192], 16
+  sequences, 32/8 heads x 128, fp16 Q/K/V through one launch with a
+  prefix-sum offset table, against the oracle.
+- Config 5 (Llama-3-8B architecture, Q4_0, 32 ragged sequences): the M=32
+  LM-head product (128256 x 4096, binary16 weights) against a float64
+  product, and a full-dimension 32-sequence step with contexts U[256, 4096]
+  against single-sequence steps of the same sequences in their own KV slots.
+
+Weights are random (synth); K-quant blocks are drawn as bytes for speed.
+"""
+import numpy as np
+import pytest
+import torch
+
+from janus_amd import _lib, ops, synth
+from janus_amd.model import Model
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+REL = 2e-3
+
+
+def _rel_err(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+def _llama2_spec(layers, seed=3):
+    # C3: hidden 4096, 32 MHA heads, FFN 11008, vocab 32000, theta 1e4,
+    # F32 embeddings, F16 LM head
+    return synth.make_model(seed, 4096, 32, 32, 11008, 32000, layers, synth.Q4_K, 1e-5, 10000.0,
+                            embed_type=synth.F32, head_type=synth.F16, kquant_bytes=True)
+
+
+@pytest.fixture(scope="module")
+def c3_two_layers():
+    return _llama2_spec(2)
+
+
+def test_config3_mha_q4k_logits_every_step(engine, c3_two_layers):
+    spec = c3_two_layers
+    prompt = np.random.default_rng(31).integers(0, spec.vocab, 12).tolist()
+    ref = O.OracleModel(spec, 32, kv_f16=True)
+    m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    worst = 0.0
+    for p, t in enumerate(prompt):
+        want = ref.forward(t, p)
+        m.forward([t], [p])
+        worst = max(worst, _rel_err(m.logits()[0], want))
+    m.close()
+    assert worst <= REL, worst
+
+
+def test_config3_mha_q4k_greedy_tokens(engine, c3_two_layers):
+    spec = c3_two_layers
+    prompt = np.random.default_rng(32).integers(0, spec.vocab, 10).tolist()
+    want = O.OracleModel(spec, 32, kv_f16=True).generate(prompt, 8, 1.15)
+    m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    got = m.generate(prompt, 8, 1.15)
+    m.close()
+    assert got == want
+
+
+def test_config3_full_model_graph_equals_eager(engine):
+    """32 layers at full size, 512-token prefill, then 8 decode steps eagerly
+    (host argmax) and 8 as captured-step replays from the same state."""
+    spec = _llama2_spec(32)
+    prompt = np.random.default_rng(3).integers(0, spec.vocab, 512).tolist()
+    m = Model(engine, spec, max_seq_len=528, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    del spec
+    for p, t in enumerate(prompt):
+        m.forward([t], [p])
+    eager, last, pos = [], prompt[-1], 512
+    for _ in range(8):
+        m.forward([last], [pos])
+        last = O.argmax_last(m.logits()[0])
+        eager.append(last)
+        pos += 1
+    m.set_sampler(_lib.SAMPLER_ARGMAX)
+    m.graph_begin([prompt[-1]], [512])
+    m.graph_run(8)
+    graph = m.generated(0)
+    m.close()
+    assert graph == eager
+
+
+def test_config4_seeded_lengths(engine):
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng(4)
+    lens = rng.integers(128, 8193, 16)
+    assert lens.max() > 4096
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    total = int(lens.sum())
+    k = rng.standard_normal((total, KVH, D), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((total, KVH, D), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((16, H * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    out = torch.empty(16, H * D, device=DEV)
+    ops.compute_attention(engine, torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
+                          torch.from_numpy(v).to(DEV), out, 16, 0, int(lens.max()), H, KVH, D,
+                          row_base=torch.from_numpy(offs).to(DEV),
+                          seq_lens=torch.from_numpy(lens.astype(np.int32)).to(DEV), max_len_hint=int(lens.max()))
+    got = out.cpu().numpy()
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    for b in range(16):
+        sl = slice(offs[b], offs[b] + lens[b])
+        want = O.attention(q[b], kf[sl], vf[sl], H, KVH, D)
+        assert np.allclose(got[b], want, rtol=2e-5, atol=2e-6), (b, int(lens[b]), float(np.max(np.abs(got[b] - want))))
+
+
+def test_config5_lm_head_m32_matches_f64(engine):
+    n, k, rows = 128256, 4096, 32
+    g = torch.Generator(device=DEV).manual_seed(5)
+    wh = (torch.randn(n, k, device=DEV, generator=g) * 0.02).to(torch.float16)
+    w = ops.GpuTensor(engine, _lib.DT_F16, n, k, wh.view(torch.int16).cpu().numpy().view(np.uint16))
+    a = torch.randn(rows, k, device=DEV, generator=g).to(torch.float16)
+    c = torch.empty(rows, n, device=DEV)
+    ops.gemm_auto(engine, a, w, c, rows, 1, k, n)
+    wf = w.dequant().double()
+    ad = a.double()
+    ref = ad @ wf.T
+    bound = 2e-5 * (ad.abs() @ wf.abs().T) + 1e-30
+    err = (c.double() - ref).abs()
+    ratio = float((err / bound).max())
+    del wf, ref, bound, err
+    assert ratio <= 1.0, ratio
+
+
+def test_config5_32_sequence_step_equals_single_runs(engine):
+    """One full-dimension ragged step: 32 sequences at positions U[256, 4096]
+    over random fp16 caches, on the fused batched path (MFMA products), against
+    the same sequences stepped alone (GEMV path) in their own KV slots."""
+    spec = synth.make_model(7, 4096, 32, 8, 14336, 128256, 32, synth.Q4_0, 1e-5, 500000.0,
+                            embed_type=synth.F16, head_type=synth.F16)
+    rng = np.random.default_rng(5)
+    lens = rng.integers(256, 4097, 32)
+    max_seq = int(lens.max()) + 1
+    m = Model(engine, spec, max_seq_len=max_seq, max_batch=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    del spec
+    shape = (32, 32 * max_seq, 8, 128)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    kc = torch.randn(shape, device=DEV, dtype=torch.float16, generator=g)
+    vc = torch.randn(shape, device=DEV, dtype=torch.float16, generator=g)
+    m.set_kv_cache(kc, vc)
+    toks = rng.integers(0, 128256, 32).tolist()
+    m.forward(toks, lens.tolist())
+    batch = m.logits(32)
+    for s in (0, 13, 31):
+        m.forward([toks[s]], [int(lens[s])], slots=[s])
+        err = _rel_err(m.logits()[0], batch[s])
+        assert err <= REL, (s, err)
+    m.close()
+    del kc, vc

@@ -1,0 +1,282 @@
+"""GPU parity of the device-side decode loop (include/janus_model.h).
+
+- generate runs on captured-step replays with the penalty's context kept as
+  occurrence counts on the device: its tokens equal the oracle's
+  Model::generate (generation.rs:129-323, sampler.rs:146-209) and a host
+  loop that samples the GPU's own logits with the oracle's sampler, over
+  200+ tokens and with both sampler rules (penalty + last max; the
+  |penalty - 1| < 0.01 fast path with argmax.wgsl's tie rule, planted ties);
+- graph decode with the penalty equals eager decode with the host sampler;
+- KV slots: a sequence gives the same logits in any slot;
+- generate_batch (continuous batching, requests admitted into freed slots)
+  gives every request the tokens it gets alone and the oracle's;
+- a workspace that grows after a capture does not invalidate the captured
+  step (the old buffer stays alive).
+"""
+import numpy as np
+import pytest
+import torch
+
+from janus_amd import _lib, ops, synth
+from janus_amd.model import Model
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _prompt(seed, n, vocab):
+    return np.random.default_rng(seed).integers(0, vocab, n).tolist()
+
+
+def _rel_err(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.fixture(scope="module")
+def spec():
+    return synth.tiny_config1(1)
+
+
+def _host_loop(m, prompt, steps, penalty):
+    """Eager decode on the GPU with the oracle's sampler on the GPU's logits."""
+    for p, t in enumerate(prompt):
+        m.forward([t], [p])
+    last, pos, gen = prompt[-1], len(prompt), []
+    for _ in range(steps):
+        m.forward([last], [pos])
+        last = O.greedy_sample(m.logits()[0], gen, penalty)
+        gen.append(last)
+        pos += 1
+    return gen
+
+
+@pytest.mark.parametrize("act", [_lib.DT_F32, _lib.DT_F16])
+def test_generate_200_tokens_penalty_matches_oracle_and_host_loop(engine, spec, act):
+    prompt = _prompt(101, 32, spec.vocab)
+    want = O.OracleModel(spec, 256).generate(prompt, 200, 1.15)
+    m = Model(engine, spec, max_seq_len=256, act_dtype=act)
+    got = m.generate(prompt, 200, repetition_penalty=1.15)
+    host = _host_loop(m, prompt, 200, 1.15)
+    m.close()
+    assert len(got) == 200
+    assert got == host
+    if act == _lib.DT_F32:
+        assert got == want
+    else:
+        # binary16 activations: the stream follows the oracle until a near tie
+        same = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), len(want))
+        assert same >= 16, same
+
+
+def _tied_head_spec(vocab=512):
+    """Config-1 architecture whose LM head is zero except rows 4 and 12 (equal
+    to w) and rows 20 and 28 (equal to -w): whatever the sign of w . x, the
+    largest logit is a tie between two rows that are equal mod 8, so both take
+    the same reduction path and tie exactly. argmax.wgsl prefers the smaller
+    bitrev8(i % 256) (4 over 12, 20 over 28), the last-max argmax the later
+    index; the zero logits tie as well (argmax.wgsl: 0, last-max: vocab-1)."""
+    s = synth.tiny_config1(3)
+    rng = np.random.default_rng(5)
+    head = np.zeros((vocab, s.hidden), np.float32)
+    row = rng.standard_normal(s.hidden).astype(np.float32) * np.float32(0.05)
+    head[4] = head[12] = row
+    head[20] = head[28] = -row
+    s.tensors = [t for t in s.tensors if t.name != "output.weight"]
+    s.tensors.append(synth.Tensor("output.weight", synth.F32, vocab, s.hidden, head))
+    return s
+
+
+@pytest.mark.parametrize("act", [_lib.DT_F32, _lib.DT_F16])
+@pytest.mark.parametrize("penalty", [1.0, 1.005, 1.15])
+def test_generate_sampler_rules_with_planted_ties(engine, act, penalty):
+    s = _tied_head_spec()
+    for seed in range(3):
+        prompt = _prompt(200 + seed, 6, s.vocab)
+        want = O.OracleModel(s, 32).generate(prompt, 6, penalty)
+        m = Model(engine, s, max_seq_len=32, act_dtype=act)
+        got = m.generate(prompt, 6, repetition_penalty=penalty)
+        m.close()
+        assert got == want, (seed, got, want)
+        # the first choice is decided by a tie rule
+        assert want[0] in ((4, 20) if penalty < 1.01 else (12, 28)), want
+
+
+def test_graph_penalty_decode_matches_eager(engine):
+    """The captured step with the penalty sampler (counts kept on the device)
+    against eager steps sampled on the host, for a batch of 3 and for 1."""
+    s = synth.make_model(41, 512, 4, 1, 1024, 1000, 2, synth.Q4_0, 1e-5, 500000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    for nseq in (1, 3):
+        prompts = [_prompt(50 + i, 7 + i, s.vocab) for i in range(nseq)]
+        outs = []
+        for use_graph in (False, True):
+            m = Model(engine, s, max_seq_len=64, max_batch=3, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+            n = max(len(p) for p in prompts)
+            for step in range(n):
+                m.forward([p[min(step, len(p) - 1)] for p in prompts], [min(step, len(p) - 1) for p in prompts])
+            last = [p[-1] for p in prompts]
+            pos = [len(p) for p in prompts]
+            gens = [[] for _ in prompts]
+            if use_graph:
+                m.set_sampler(_lib.SAMPLER_PENALTY, 1.15)
+                m.graph_begin(last, pos)
+                m.graph_run(12)
+                gens = [m.generated(r) for r in range(nseq)]
+            else:
+                for _ in range(12):
+                    m.forward(last, pos)
+                    lg = m.logits(nseq)
+                    last = [O.greedy_sample(lg[r], gens[r], 1.15) for r in range(nseq)]
+                    for r in range(nseq):
+                        gens[r].append(last[r])
+                    pos = [p + 1 for p in pos]
+            outs.append(gens)
+            m.close()
+        assert outs[0] == outs[1], nseq
+
+
+def test_kv_slots_equal_logits(engine, spec):
+    prompt = _prompt(61, 9, spec.vocab)
+    m = Model(engine, spec, max_seq_len=32, max_batch=4)
+    out = []
+    for slot in (0, 2, 3):
+        for p, t in enumerate(prompt):
+            m.forward([t], [p], slots=[slot])
+        out.append(m.logits()[0])
+    # two sequences in swapped slots in one batch
+    other = _prompt(62, 9, spec.vocab)
+    for p in range(9):
+        m.forward([other[p], prompt[p]], [p, p], slots=[3, 1])
+    both = m.logits(2)
+    m.close()
+    assert np.array_equal(out[0], out[1]) and np.array_equal(out[0], out[2])
+    assert _rel_err(both[1], out[0]) <= 1e-5
+
+
+def test_kv_slots_rejects_bad_slots(engine, spec):
+    m = Model(engine, spec, max_seq_len=32, max_batch=2)
+    with pytest.raises(ops.JanusError):
+        m.forward([1, 2], [0, 0], slots=[1, 1])
+    with pytest.raises(ops.JanusError):
+        m.forward([1], [0], slots=[2])
+    m.close()
+
+
+@pytest.mark.parametrize("act,kv", [(_lib.DT_F32, _lib.DT_F32), (_lib.DT_F16, _lib.DT_F16)])
+def test_generate_batch_continuous_matches_alone_and_oracle(engine, spec, act, kv):
+    """7 requests of different lengths through 3 slots: requests finish at
+    different steps and waiting ones take their slots mid-run."""
+    rng = np.random.default_rng(71)
+    lens = [5, 12, 3, 9, 1, 7, 4]
+    maxt = 9
+    prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
+    m = Model(engine, spec, max_seq_len=48, max_batch=3, kv_dtype=kv, act_dtype=act)
+    got = m.generate_batch(prompts, maxt, 1.15)
+    alone = [m.generate_batch([p], maxt, 1.15)[0] for p in prompts]
+    m.close()
+    assert all(len(g) == maxt for g in got)
+    for p, g, a in zip(prompts, got, alone):
+        want = O.OracleModel(spec, 48, kv_f16=(kv == _lib.DT_F16)).generate(p, maxt, 1.15, batch_rules=True)
+        if act == _lib.DT_F32:
+            # f32 activations: batched rows run the per-row products of a
+            # single sequence, so only attention's split plan differs
+            assert g == a
+            assert g == want
+        else:
+            # binary16 activations: batched rows take the MFMA products,
+            # alone the GEMV ones (fp32 sums in another order)
+            for other in (a, want):
+                same = next((i for i, (x, y) in enumerate(zip(g, other)) if x != y), maxt)
+                assert same >= 4, (same, g, other)
+
+
+def test_generate_batch_capacity_and_empty_prompt(engine, spec):
+    m = Model(engine, spec, max_seq_len=16, max_batch=2)
+    out = m.generate_batch([[1, 2, 3], list(range(14)), [5]], 8, 1.15)
+    assert [len(o) for o in out] == [8, 2, 8]   # positions 14 and 15 only for the long prompt
+    with pytest.raises(ops.JanusError):
+        m.generate_batch([[1], []], 4, 1.15)
+    m.close()
+
+
+def _eos_spec():
+    """Vocabulary of 128256 with an LM head that is zero except row 128009, set
+    to the sign pattern of the first decode step's normalised hidden state of
+    prompt A: A's first sampled token is the stop token 128009; for other
+    prompts the oracle decides."""
+    s = synth.make_model(83, 256, 4, 2, 512, 128256, 1, synth.Q8_0, 1e-5, 10000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    return s
+
+
+def test_stop_token_generate_drops_batch_keeps(engine):
+    s = _eos_spec()
+    pa = [11, 22, 33]
+    ref = O.OracleModel(s, 16)
+    for p, t in enumerate(pa):
+        ref.forward(t, p)
+    # the normalised hidden of the decode step at position 3 (token 33)
+    xs = {}
+    orig = O.rmsnorm
+
+    def spy(x, gamma, eps):
+        xs["last"] = np.array(x, copy=True)
+        return orig(x, gamma, eps)
+
+    O.rmsnorm = spy
+    try:
+        ref.forward(33, 3)
+    finally:
+        O.rmsnorm = orig
+    xn = O.rmsnorm(xs["last"], [t for t in s.tensors if t.name == "output_norm.weight"][0].data, s.rms_eps)
+    head = np.zeros((s.vocab, s.hidden), np.float32)
+    head[128009] = np.sign(xn) * np.float32(0.05)
+    head[77] = np.sign(xn) * np.float32(0.01)
+    s.tensors = [t for t in s.tensors if t.name != "output.weight"]
+    s.tensors.append(synth.Tensor("output.weight", synth.F16, s.vocab, s.hidden, synth.f16_bits(head)))
+    want_single = O.OracleModel(s, 16).generate(pa, 5, 1.15)
+    want_batch = O.OracleModel(s, 16).generate(pa, 5, 1.15, batch_rules=True)
+    assert want_single == [] and want_batch == [128009]
+    pb = [5, 6, 7, 8]
+    want_b = O.OracleModel(s, 16).generate(pb, 5, 1.15, batch_rules=True)
+    m = Model(engine, s, max_seq_len=16, max_batch=2)
+    assert m.generate(pa, 5, 1.15) == want_single
+    assert m.generate_batch([pa, pb], 5, 1.15) == [want_batch, want_b]
+    m.close()
+
+
+def test_workspace_growth_keeps_captured_step(engine):
+    """Capture with fewer sequences than max_batch, grow the GEMM workspace
+    with a large standalone product, then replay: the captured step must
+    still give the eager tokens (its workspace was retired, not freed)."""
+    s = synth.make_model(91, 512, 4, 1, 1024, 1000, 2, synth.Q4_0, 1e-5, 500000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    prompts = [_prompt(92, 6, s.vocab), _prompt(93, 6, s.vocab)]
+    outs = []
+    for grow in (False, True):
+        m = Model(engine, s, max_seq_len=48, max_batch=4, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for step in range(6):
+            m.forward([p[step] for p in prompts], [step, step])
+        m.graph_begin([p[-1] for p in prompts], [6, 6])
+        m.graph_run(3)
+        if grow:
+            _, before = engine.workspace_bytes()
+            n, k = 32768, 4096
+            w = ops.GpuTensor(engine, 1, n, k, synth.f16_bits(np.full((n, k), 0.01, np.float32)))
+            a = torch.ones(64, k, device=DEV, dtype=torch.float16)
+            c = torch.empty(64, n, device=DEV)
+            ops.gemm_auto(engine, a, w, c, 64, 1, k, n)
+            engine.sync()
+            _, after = engine.workspace_bytes()
+            assert after > before
+            # eager steps with every row in between (another plan, same buffers)
+            m2 = Model(engine, s, max_seq_len=48, max_batch=4, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+            m2.forward([1, 2, 3, 4], [0, 0, 0, 0])
+            m2.close()
+            del w
+        m.graph_run(6)
+        outs.append([m.generated(r) for r in range(2)])
+        m.close()
+    assert outs[0] == outs[1]
+    assert all(len(g) == 9 for g in outs[0])
