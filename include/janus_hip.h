@@ -194,6 +194,21 @@ int janus_attention(janus_ctx *ctx, const float *q, const void *k_cache, const v
                     uint32_t kv_heads, uint32_t head_dim, uint32_t seq_len,
                     uint32_t max_seq_len, const int32_t *d_row_base,
                     const int32_t *d_seq_lens, uint32_t max_len_hint, float scale);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): janus_attention with the same arguments, kernels and
+ * results, whose split partials go to a fixed per-device scratch of
+ * JANUS_ATTN_SCRATCH_BYTES held for the life of the process, so the call
+ * allocates nothing. A shape whose partials need more than that is rejected
+ * with JANUS_E_INVALID_DIM before anything is enqueued. Every call on a
+ * device shares that device's scratch: calls that overlap on one GPU (two
+ * streams, or two contexts on different threads) race on it. */
+#define JANUS_ATTN_SCRATCH_BYTES (16u << 20)
+int janus_attention_noalloc(janus_ctx *ctx, const float *q, const void *k_cache, const void *v_cache,
+                            int kv_dtype, float *out, uint32_t batch, uint32_t heads,
+                            uint32_t kv_heads, uint32_t head_dim, uint32_t seq_len,
+                            uint32_t max_seq_len, const int32_t *d_row_base,
+                            const int32_t *d_seq_lens, uint32_t max_len_hint, float scale);
 
 /* ---- embedding (model/transformer/embedding.rs:16-198) ---------------- */
 /* out[b][:] = table[ids[b]][:] decoded as the table's binary16 values.

@@ -38,6 +38,7 @@ TIE_WGSL = 1
 SAMPLER_ARGMAX = 0
 SAMPLER_PENALTY = 1
 SAMPLER_WGSL = 2
+ATTN_SCRATCH_BYTES = 16 << 20
 
 P = C.c_void_p
 U32 = C.c_uint32
@@ -91,6 +92,7 @@ _SIGNATURES = {
     "janus_rope": (I32, [P, P, P, P, U32, U32, U32, U32, P]),
     "janus_kv_update": (I32, [P, P, P, P, P, I32, U32, U32, U32, U32, U32, P, P]),
     "janus_attention": (I32, [P, P, P, P, I32, P, U32, U32, U32, U32, U32, U32, P, P, U32, F32]),
+    "janus_attention_noalloc": (I32, [P, P, P, P, I32, P, U32, U32, U32, U32, U32, U32, P, P, U32, F32]),
     "janus_embed": (I32, [P, P, P, U32, P]),
     "janus_embed_device": (I32, [P, P, P, U32, P]),
     "janus_argmax": (I32, [P, P, P, U32, U32, I32]),

@@ -18,6 +18,7 @@
 //    directly.
 //  * Ragged batches: per-sequence row offsets and lengths are device tables,
 //    so all sequences share one launch.
+#include <mutex>
 #include <type_traits>
 
 #include "internal.h"
@@ -678,6 +679,31 @@ int attention_reserve(janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t k
                       uint32_t max_len, int kv_f16) {
     const size_t bytes = attention_ws_bytes(ctx, batch, heads, kv_heads, hd, max_len, kv_f16);
     return bytes ? ensure_attn_ws(ctx, bytes) : JANUS_OK;
+}
+
+// ---- fixed scratch for the allocation-free entry point -------------------------
+// The split partials of janus_attention_noalloc live in this array, one copy
+// per device for the life of the process. Host code never passes the array's
+// name to a kernel or a copy: it uses the device address that
+// attention_scratch_init obtains per device with hipGetSymbolAddress.
+static __device__ __align__(256) float scratch[kAttnScratchBytes / sizeof(float)];
+
+namespace {
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+int attention_scratch_init(janus_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxScratchDevices) return JANUS_OK;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ctx->device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(attention scratch)");
+        g_scratch_ptr[ctx->device] = (float *)p;
+    }
+    ctx->attn_scratch = g_scratch_ptr[ctx->device];
+    return JANUS_OK;
 }
 
 int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void *vc, int kv_dt, void *out,

@@ -48,7 +48,16 @@ struct janus_ctx {
     // Workspaces replaced by a larger one. A captured graph may still write
     // them, so they are freed only by janus_destroy.
     std::vector<void *> retired;
+    // Device address of this device's fixed attention scratch (the
+    // allocation-free entry point), or null if the lookup failed.
+    float *attn_scratch = nullptr;
+    std::string attn_scratch_error;
 };
+
+// Size of the fixed attention scratch: one per device, held for the life of
+// the process. Split partials of up to this many bytes run allocation-free.
+constexpr size_t kAttnScratchBytes = JANUS_ATTN_SCRATCH_BYTES;
+constexpr int kMaxScratchDevices = 64;
 
 // Greedy sampler state in device memory, read by the argmax kernels, so a
 // captured decode step follows a change without being captured again.
@@ -202,6 +211,10 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
                      uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t seq_len,
                      uint32_t max_seq, const int32_t *row_base, const int32_t *seq_lens, uint32_t max_len,
                      float scale, int out_f16 = 0, float *fixed_ws = nullptr, size_t fixed_ws_bytes = 0);
+// Looks up, once per device, the device address of the fixed attention
+// scratch (kAttnScratchBytes) and stores it in ctx->attn_scratch. Called by
+// janus_create with the context's device current.
+int attention_scratch_init(janus_ctx *ctx);
 int embed_launch(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, const int32_t *d_ids,
                  uint32_t batch, float *out);
 int argmax_launch(janus_ctx *ctx, const float *logits, int32_t *out, uint32_t vocab, uint32_t batch, int tie);

@@ -163,6 +163,30 @@ int janus_attention(janus_ctx *ctx, const float *q, const void *k_cache, const v
                             d_row_base, d_seq_lens, max_len, scale);
 }
 
+int janus_attention_noalloc(janus_ctx *ctx, const float *q, const void *k_cache, const void *v_cache, int kv_dt,
+                            float *out, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                            uint32_t seq_len, uint32_t max_seq_len, const int32_t *d_row_base,
+                            const int32_t *d_seq_lens, uint32_t max_len_hint, float scale) {
+    if (check_ctx(ctx)) return JANUS_E_INVALID_ARG;
+    if (int e = attention_args(ctx, q, k_cache, v_cache, kv_dt, out, heads, kv_heads, hd, seq_len, max_seq_len,
+                               d_seq_lens))
+        return e;
+    if (batch == 0) return JANUS_OK;
+    const uint32_t max_len = d_seq_lens ? (max_len_hint ? max_len_hint : max_seq_len) : seq_len;
+    // the same split plan as janus_attention, checked against the fixed scratch on the host
+    const size_t need = attention_ws_bytes(ctx, batch, heads, kv_heads, hd, max_len, kv_dt == JANUS_DT_F16);
+    if (need > kAttnScratchBytes)
+        return fail(ctx, JANUS_E_INVALID_DIM,
+                    "attention_noalloc: split partials need " + std::to_string(need) + " bytes, above the " +
+                        std::to_string(kAttnScratchBytes) + "-byte fixed scratch; use janus_attention");
+    if (int e = need_device(ctx)) return e;
+    if (!ctx->attn_scratch)
+        return fail(ctx, JANUS_E_HIP, "attention_noalloc: no fixed scratch on this device: " + ctx->attn_scratch_error);
+    if (scale <= 0.0f) scale = 1.0f / sqrtf((float)hd);
+    return attention_launch(ctx, q, k_cache, v_cache, kv_dt, out, batch, heads, kv_heads, hd, seq_len, max_seq_len,
+                            d_row_base, d_seq_lens, max_len, scale, 0, ctx->attn_scratch, kAttnScratchBytes);
+}
+
 int janus_embed(janus_ctx *ctx, const janus_weight *table, const uint32_t *h_ids, uint32_t batch, float *out) {
     if (check_ctx(ctx)) return JANUS_E_INVALID_ARG;
     if (!table || !h_ids || !out) return fail(ctx, JANUS_E_INVALID_ARG, "embed: null argument");

@@ -303,6 +303,12 @@ int janus_create(int hip_device, janus_ctx **out) {
         return JANUS_E_HIP;
     }
     ctx->stream = ctx->own_stream;
+    // the allocation-free attention entry point's scratch: its device address
+    // on this device (a failure is reported by that entry point)
+    if (attention_scratch_init(ctx) != JANUS_OK) {
+        ctx->attn_scratch_error = ctx->last_error;
+        ctx->last_error.clear();
+    }
     if (const char *k = std::getenv("JANUS_GEMV_KERNEL")) ctx->gemv_lds = std::strcmp(k, "reg") != 0;
     if (const char *k = std::getenv("JANUS_ATTN_KERNEL")) ctx->attn_valu = std::strcmp(k, "valu") == 0;
     if (const char *k = std::getenv("JANUS_ATTN_WPC")) {

@@ -234,6 +234,18 @@ def compute_attention(engine, query, key_cache, value_cache, output, batch_size:
         scale))
 
 
+def compute_attention_noalloc(engine, query, key_cache, value_cache, output, batch_size: int, seq_len: int,
+                              max_seq_len: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                              row_base: Optional[torch.Tensor] = None, seq_lens: Optional[torch.Tensor] = None,
+                              max_len_hint: int = 0, scale: float = 0.0) -> None:
+    """compute_attention through the allocation-free entry point (fixed
+    per-device scratch; janus_attention_noalloc in include/janus_hip.h)."""
+    engine._check(engine.lib.janus_attention_noalloc(
+        engine.ctx, _ptr(query), _ptr(key_cache), _ptr(value_cache), _dt(key_cache), _ptr(output), batch_size,
+        num_heads, num_kv_heads, head_dim, seq_len, max_seq_len, _ptr(row_base), _ptr(seq_lens), max_len_hint,
+        scale))
+
+
 # ---- embedding and sampling ---------------------------------------------------------
 
 def embed_tokens(engine, table: GpuTensor, token_ids: Sequence[int], output) -> None:
