@@ -142,19 +142,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
     // per-query-head launch (short contexts): one head per workgroup, KV head y / qh_div
     const uint32_t kvh = a.qh_div ? blockIdx.y / a.qh_div : blockIdx.y;
     const uint32_t h0 = a.qh_div ? blockIdx.y : blockIdx.y * G;   // first query head of this workgroup
-    // lengths beyond the planned splits (or the capacity) are clamped, never read past
-    const uint32_t span = (uint32_t)nw * a.chunk;
-    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * span);
-    const uint32_t wg_start = split * span;
-    if (wg_start >= len && !(split == 0 && len == 0)) return;   // whole workgroup; len 0: split 0 writes zeros
-    const uint32_t wg_end = min(len, wg_start + span);
-    const uint32_t start = wg_start + wave * a.chunk;
-    const uint32_t end = min(wg_end, start + a.chunk);
-    const size_t row0 = (size_t)(a.row_base ? (uint32_t)a.row_base[b] : b * a.max_seq);
-    const uint32_t kvrow = a.kv_heads * D;
-    const KV *kc = (const KV *)a.kc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
-    const KV *vc = (const KV *)a.vc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
-
+    // The sequence's length and row base are requested together, before
+    // anything waits on either (one round trip, not one per value).
+    const uint32_t len_raw = a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len;
+    const uint32_t base_raw = a.row_base ? (uint32_t)a.row_base[b] : b * a.max_seq;
     float qr[G][8], acc[G][8], m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -167,6 +158,18 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
         m[g] = -INFINITY;
         l[g] = 0.0f;
     }
+    // lengths beyond the planned splits (or the capacity) are clamped, never read past
+    const uint32_t span = (uint32_t)nw * a.chunk;
+    const uint32_t len = min(min(len_raw, a.max_seq), a.splits * span);
+    const uint32_t wg_start = split * span;
+    if (wg_start >= len && !(split == 0 && len == 0)) return;   // whole workgroup; len 0: split 0 writes zeros
+    const uint32_t wg_end = min(len, wg_start + span);
+    const uint32_t start = wg_start + wave * a.chunk;
+    const uint32_t end = min(wg_end, start + a.chunk);
+    const size_t row0 = (size_t)base_raw;
+    const uint32_t kvrow = a.kv_heads * D;
+    const KV *kc = (const KV *)a.kc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
+    const KV *vc = (const KV *)a.vc + row0 * kvrow + (size_t)kvh * D + 8 * dl;
 
     KVRow<KV> ka[U], va[U], kb[U], vb[U];
     auto load = [&](KVRow<KV> (&k)[U], KVRow<KV> (&v)[U], uint32_t p0) {

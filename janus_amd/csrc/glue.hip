@@ -64,12 +64,12 @@ __global__ __launch_bounds__(256) void rmsnorm_long_kernel(const float *__restri
     __shared__ float red[4];
     const float *x = in + (size_t)blockIdx.x * hidden;
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) s = fmaf(x[i], x[i], s);
+    for (uint32_t i = threadIdx.x; i < hidden; i += 256u) s = fmaf(x[i], x[i], s);
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     const float rms = sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden + eps);
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < hidden; i += 256u) {
         float v = (x[i] / rms) * gamma[i];
         if (OUT_F16) ((uint16_t *)out)[(size_t)blockIdx.x * hidden + i] = f2h_bits(v);
         else ((float *)out)[(size_t)blockIdx.x * hidden + i] = v;
@@ -99,7 +99,7 @@ __device__ __forceinline__ float silu_f(float x) { return x * (1.0f / (1.0f + ex
 template <int OP, bool OUT_F16>
 __global__ __launch_bounds__(256) void elementwise_kernel(const float *__restrict__ a, const float *__restrict__ b,
                                                           void *__restrict__ out, uint32_t n) {
-    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= n) return;
     float v;
     if (OP == EW_SILU) v = silu_f(a[i]);
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const float *in, float *out, 
                                                    uint32_t batch, uint32_t heads, uint32_t hd,
                                                    uint32_t position, const int32_t *__restrict__ positions) {
     const uint32_t half = hd / 2;
-    uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= batch * heads * half) return;
     uint32_t b = idx / (heads * half), rem = idx % (heads * half);
     uint32_t h = rem / half, i = rem % half;
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const float *__restrict_
                                                         uint32_t row_elems, uint32_t position, uint32_t max_seq,
                                                         const int32_t *__restrict__ row_base,
                                                         const int32_t *__restrict__ positions) {
-    uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= batch * row_elems) return;
     uint32_t b = idx / row_elems, e = idx % row_elems;
     const uint32_t pos = positions ? (uint32_t)positions[b] : position;
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t *__restrict__
     const uint32_t b = blockIdx.y;
     const int32_t id = d_ids ? d_ids[b] : ids.id[b];
     float *o = out + (size_t)b * hidden;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < hidden; i += gridDim.x * 256u)
         o[i] = ((uint32_t)id < vocab) ? h2f(table[(size_t)id * hidden + i]) : 0.0f;
 }
 
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(1024) void argmax_last_kernel(const float *__restri
     const float *l = logits + (size_t)blockIdx.x * vocab;
     float bv = -INFINITY;
     int32_t bi = -1;
-    for (uint32_t i = threadIdx.x; i < vocab; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < vocab; i += 1024u) {
         float v = l[i];
         if (v > bv || (v == bv && (int32_t)i > bi)) { bv = v; bi = (int32_t)i; }
     }
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(1024) void argmax_last_kernel(const float *__restri
     if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+        for (int w = 1; w < 16; ++w)
             if (sv[w] > bv || (sv[w] == bv && si[w] > bi)) { bv = sv[w]; bi = si[w]; }
         out[blockIdx.x] = bi < 0 ? 0 : bi;
     }
@@ -301,32 +301,43 @@ __global__ __launch_bounds__(1024) void argmax_keys_kernel(const float *__restri
     const uint32_t base = blockIdx.x * 32768u + threadIdx.x * 4u;
     uint64_t key = 0;
     float4 v[8];
+    uint4 c[8];
     const bool vec = (vocab & 3u) == 0;
+    const bool counted = mode == SAMPLE_PENALTY && cnt;
+    // logits and (under the penalty) their counts requested together
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t i = base + 4096u * j;
+        c[j] = make_uint4(0u, 0u, 0u, 0u);
         if (vec && i + 4 <= vocab) {
             v[j] = *(const float4 *)(l + i);
+            if (counted) c[j] = *(const uint4 *)(cnt + i);
         } else {
             v[j].x = i < vocab ? l[i] : -INFINITY;
             v[j].y = i + 1 < vocab ? l[i + 1] : -INFINITY;
             v[j].z = i + 2 < vocab ? l[i + 2] : -INFINITY;
             v[j].w = i + 3 < vocab ? l[i + 3] : -INFINITY;
+            if (counted) {
+                c[j].x = i < vocab ? cnt[i] : 0u;
+                c[j].y = i + 1 < vocab ? cnt[i + 1] : 0u;
+                c[j].z = i + 2 < vocab ? cnt[i + 2] : 0u;
+                c[j].w = i + 3 < vocab ? cnt[i + 3] : 0u;
+            }
         }
     }
-    auto take = [&](float x, uint32_t i) {
+    auto take = [&](float x, uint32_t i, uint32_t n) {
         if (i < vocab) {
-            const uint64_t k = sampler_key(x, i, cnt, mode, pen);
+            const uint64_t k = sampler_key(x, i, n, mode, pen);
             key = k > key ? k : key;
         }
     };
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t i = base + 4096u * j;
-        take(v[j].x, i);
-        take(v[j].y, i + 1);
-        take(v[j].z, i + 2);
-        take(v[j].w, i + 3);
+        take(v[j].x, i, c[j].x);
+        take(v[j].y, i + 1, c[j].y);
+        take(v[j].z, i + 2, c[j].z);
+        take(v[j].w, i + 3, c[j].w);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {

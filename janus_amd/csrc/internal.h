@@ -29,6 +29,7 @@ struct janus_ctx {
     // JANUS_GEMV_LDS_WPC)
     uint32_t gemv_wpc = 16;
     uint32_t gemv_lds_wpc = 16;
+    uint32_t gemv_lds_threads = 0;   // LDS GEMV workgroup size (0: chosen per launch)
     // binary16-cache attention scores on MFMA (JANUS_ATTN_KERNEL=valu selects
     // the all-VALU kernel instead, for comparisons).
     bool attn_valu = false;
@@ -292,7 +293,7 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 
 // Argmax key of logit v at index idx under the sampler state s.
 //  SAMPLE_PENALTY: v first takes the repetition penalty once per occurrence
-//    of idx among the generated tokens (counts[idx]; sampler.rs:599-613:
+//    of idx among the generated tokens (count; sampler.rs:599-613:
 //    divide when positive, else multiply). Occurrences of one id are applied
 //    in order and ids do not interact, so this equals the reference's loop
 //    over the context. Then the last-max key.
@@ -300,7 +301,7 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 //    wins, and values not above -1e38 (or NaN) count as -1e38 at index 0:
 //    the per-lane strict '>' scan from -1e38 and the strict '>' tree of
 //    shaders/argmax.wgsl:26-126. Index below 2^24.
-__device__ __forceinline__ uint64_t sampler_key(float v, uint32_t idx, const uint32_t *counts, int mode,
+__device__ __forceinline__ uint64_t sampler_key(float v, uint32_t idx, uint32_t count, int mode,
                                                 float penalty) {
     if (mode == SAMPLE_WGSL) {
         if (!(v > -1e38f)) {
@@ -312,8 +313,8 @@ __device__ __forceinline__ uint64_t sampler_key(float v, uint32_t idx, const uin
         const uint32_t pri = (__builtin_bitreverse32(idx & 255u) & 0xff000000u) | idx;
         return ((uint64_t)k << 32) | (uint32_t)~pri;
     }
-    if (mode == SAMPLE_PENALTY && counts)
-        for (uint32_t c = counts[idx]; c; --c) v = v > 0.0f ? v / penalty : v * penalty;
+    if (mode == SAMPLE_PENALTY)
+        for (uint32_t c = count; c; --c) v = v > 0.0f ? v / penalty : v * penalty;
     return argmax_key(v, idx);
 }
 

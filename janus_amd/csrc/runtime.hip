@@ -323,6 +323,10 @@ int janus_create(int hip_device, janus_ctx **out) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 8 && v <= 64) ctx->gemv_lds_wpc = (uint32_t)v;
     }
+    if (const char *k = std::getenv("JANUS_GEMV_LDS_THREADS")) {
+        const int v = std::atoi(k);
+        if (v == 512 || v == 1024) ctx->gemv_lds_threads = (uint32_t)v;
+    }
     if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
         const long v = std::strtol(k, nullptr, 10);

@@ -402,7 +402,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
         if (SUMS) {
             __syncthreads();
             const uint32_t nsub = (c1 - c0) * F::CK / 32;
-            for (uint32_t i = threadIdx.x; i < nsub * Mpad; i += blockDim.x) {
+            for (uint32_t i = threadIdx.x; i < nsub * Mpad; i += 64u * WAVES * KW) {
                 const uint32_t sub = i / Mpad, m = i % Mpad;
                 const _Float16 *p8 = As + (size_t)m * a.pitch + sub * 32;
                 float s = 0.0f;
