@@ -1,15 +1,18 @@
 """ctypes binding of libjanus_hip.so (declarations: include/janus_hip.h,
 include/janus_model.h).
 
-The library is loaded from this package directory. There is no fallback: if
-the shared object is missing the import fails loudly with the build command.
+The library is loaded from this package directory (JANUS_LIB names another
+build of it, such as the host-sanitised one of `python -m janus_amd.build
+--sanitize`). There is no fallback: if the shared object is missing the
+import fails loudly with the build command.
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libjanus_hip.so"
+LIB_PATH = Path(os.environ.get("JANUS_LIB") or Path(__file__).resolve().parent / "libjanus_hip.so")
 
 # status codes (janus_status)
 OK = 0

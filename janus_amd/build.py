@@ -5,6 +5,9 @@ file in parallel, then linked as a shared object next to this package so the
 GPU box loads it straight from the repository tree.
 
 Usage: python -m janus_amd.build [--jobs N] [--no-oracle] [--incremental]
+       python -m janus_amd.build --sanitize   (host code under AddressSanitizer and
+       UndefinedBehaviorSanitizer, device code as usual, into
+       _build_san/libjanus_hip_san.so for the CPU test run of tests/run_sanitizers.sh)
 """
 from __future__ import annotations
 
@@ -21,6 +24,11 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libjanus_hip.so"
+BUILD_SAN = PKG / "_build_san"
+LIB_SAN = BUILD_SAN / "libjanus_hip_san.so"
+# host-only sanitizers: each flag goes to the host compilation alone
+SAN_FLAGS = [f for kind in ("address", "undefined") for f in ("-Xarch_host", f"-fsanitize={kind}")] + [
+    "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
 ORACLE_DIR = ROOT / "oracle"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -43,9 +51,9 @@ def _sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, out_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    obj = out_dir / (src.stem + ".o")
+    cmd = [HIPCC, *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -85,6 +93,21 @@ def build_library(jobs: int | None = None, verbose: bool = True, incremental: bo
     return LIB
 
 
+def build_sanitized(jobs: int | None = None) -> Path:
+    """The library with host code under ASan + UBSan (device code unchanged),
+    for CPU runs of the host-side validation; never loaded by default."""
+    BUILD_SAN.mkdir(exist_ok=True)
+    srcs = _sources()
+    with cf.ThreadPoolExecutor(max_workers=jobs or min(8, os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, BUILD_SAN, tuple(SAN_FLAGS)), srcs))
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *SAN_FLAGS, "-o", str(LIB_SAN), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{res.stdout}\n{res.stderr}")
+    print(f"[janus_amd.build] built {LIB_SAN.relative_to(ROOT)} (host ASan + UBSan)", flush=True)
+    return LIB_SAN
+
+
 def build_oracle(verbose: bool = True) -> Path:
     """Compile the CPU oracle (test infrastructure) with its Makefile."""
     res = subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), "-B", "liboracle.so"],
@@ -101,7 +124,11 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--no-oracle", action="store_true")
     ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
+    ap.add_argument("--sanitize", action="store_true", help="build only the host-sanitised library")
     args = ap.parse_args(argv)
+    if args.sanitize:
+        build_sanitized(args.jobs)
+        return 0
     build_library(args.jobs, incremental=args.incremental)
     if not args.no_oracle:
         build_oracle()

@@ -16,13 +16,15 @@ last-max argmax).
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# JANUS_ORACLE_LIB: another build of the oracle (the sanitised one of `make asan`)
+LIB_PATH = Path(os.environ.get("JANUS_ORACLE_LIB") or HERE / "liboracle.so")
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")

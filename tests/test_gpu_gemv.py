@@ -81,11 +81,17 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
-@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704)])
+@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704), (1003, 4096), (8200, 4096)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
-    """(1003, 8704): the LDS-staged kernel with five units per lane (the
-    single-buffered body for K-quants, double-buffered otherwise) and a last
-    workgroup whose five idle wavefronts stream a real row group and discard it."""
+    """Every binary16 product of 64+ units per row runs the LDS-staged kernel.
+    (1003, 8704): five units per lane, single-buffered (Q4_0 / Q8_0 with x
+    requested first, K-quants re-reading x from LDS; F16 rows of 1088 units take
+    the register kernel), a last 512-thread workgroup with five idle wavefronts
+    that stream a real row group and discard it. (1003, 4096): F16 with eight
+    units per lane on the double-buffered body, five idle wavefronts; the
+    quantised formats two units per lane, two idle wavefronts. (8200, 4096):
+    4100 row groups of two, enough for 1024-thread workgroups (Q4_0), whose
+    persistent grid gives some wavefronts a second group."""
     raw, w = _weight(engine, ggml_type, n, k, 3 * n + k, FTZ[ggml_type])
     rng = np.random.default_rng(n)
     xh = rng.standard_normal(k).astype(np.float16)

@@ -186,3 +186,39 @@ def test_q5_k_gemv_close_to_f64():
     ref = wf.astype(np.float64) @ x.astype(np.float64)
     bound = 1e-5 * (np.abs(wf) @ np.abs(x))
     assert np.all(np.abs(y - ref) <= bound)
+
+
+def _q6_k_ggml_numpy(raw: np.ndarray) -> np.ndarray:
+    """GGML's published block_q6_K placement, restated element by element in
+    numpy (independent of the oracle's loop): element e = 128 h + 32 j + l of a
+    block (h < 2, j < 4, l < 32) takes the low (j < 2) or high (j >= 2) nibble
+    of ql[64 h + l + 32 (j % 2)], bits 2 j..2 j + 1 of qh[32 h + l], and the
+    int8 scale sc[8 h + l // 16 + 2 j]; w = d * sc * (q - 32) in binary32."""
+    blk = raw.reshape(-1, 210)
+    e = np.arange(256)
+    h, j, l = e // 128, (e % 128) // 32, e % 32
+    ql = blk[:, 64 * h + l + 32 * (j % 2)]
+    lo = np.where(j < 2, ql & 15, ql >> 4).astype(np.int32)
+    hi = ((blk[:, 128 + 32 * h + l] >> (2 * j)) & 3).astype(np.int32)
+    sc = blk[:, 192:208].view(np.int8)[:, 8 * h + l // 16 + 2 * j].astype(np.float32)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float32)
+    q = ((hi << 4) | lo) - 32
+    return ((d * sc) * q.astype(np.float32)).reshape(-1)
+
+
+def test_q6_k_ggml_order_matches_independent_numpy_dequant():
+    """Every element and every scale group of random blocks: the oracle's GGML
+    order equals the numpy restatement bit for bit (a swapped l + 32 / l + 64
+    placement or scale group would differ on random bytes)."""
+    rng = np.random.default_rng(61)
+    nb = 64
+    raw = rng.integers(0, 256, nb * 210, dtype=np.uint8).reshape(nb, 210)
+    # finite binary16 scales d spanning several binades, some negative
+    raw[:, 208:210] = (rng.uniform(-2.0, 2.0, nb) * 2.0 ** rng.integers(-14, 4, nb)).astype(np.float16).reshape(nb, 1).view(np.uint8)
+    raw = raw.reshape(-1)
+    got = O.dequant(Q6_K, raw, nb, 256).reshape(-1)
+    want = _q6_k_ggml_numpy(raw)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # and the two placements are not the same function (the test can fail)
+    ref = O.dequant(Q6_K, raw, nb, 256, q6k_ref_order=True).reshape(-1)
+    assert np.count_nonzero(ref != want) > 200 * nb
