@@ -411,10 +411,11 @@ struct FQ4_K {
     }
     // ru: first unit of the row (a multiple of 8, uniform), u: unit in the row
     __device__ static W load_row(WPtr w, size_t ru, uint32_t u) {
-        const uint8_t *blk = w.qs + (ru >> 3) * 144;
+        const uint8_t *row = w.qs + (ru >> 3) * 144;   // uniform; one 32-bit lane offset per load
+        const uint32_t ob = (u >> 3) * 144u;
         W r;
-        r.hw = *(const uint32_t *)(blk + (u >> 3) * 144u + 4u * (__lane_id() & 3));
-        r.q = ld_stream(blk + (u >> 3) * 144u + 16u + 16u * (u & 7u));
+        r.hw = *(const uint32_t *)(row + (ob + 4u * (__lane_id() & 3)));
+        r.q = ld_stream(row + (ob + 16u + 16u * (u & 7u)));
         return r;
     }
     template <int T> __device__ static uint32_t quad_word(uint32_t v) {
@@ -561,16 +562,16 @@ struct FQ4_K {
 struct FQ5_K : FQ4_K {
     struct W { uint4 q; uint32_t qh; uint32_t hw; };
     __device__ static W load_row(WPtr w, size_t ru, uint32_t u) {
-        const uint8_t *blk = w.qs + (ru >> 3) * 176 + (u >> 3) * 176u;
-        const uint32_t c = u & 7u;
+        const uint8_t *row = w.qs + (ru >> 3) * 176;   // uniform; one 32-bit lane offset per load
+        const uint32_t ob = (u >> 3) * 176u, c = u & 7u;
         W r;
-        r.hw = *(const uint32_t *)(blk + 4u * (__lane_id() & 3));
+        r.hw = *(const uint32_t *)(row + (ob + 4u * (__lane_id() & 3)));
 #if !defined(JANUS_GEMV_NT) || JANUS_GEMV_NT
-        r.qh = __builtin_nontemporal_load((const uint32_t *)(blk + 16u + 4u * c));
+        r.qh = __builtin_nontemporal_load((const uint32_t *)(row + (ob + 16u + 4u * c)));
 #else
-        r.qh = *(const uint32_t *)(blk + 16u + 4u * c);
+        r.qh = *(const uint32_t *)(row + (ob + 16u + 4u * c));
 #endif
-        r.q = ld_stream(blk + 48u + 16u * c);
+        r.q = ld_stream(row + (ob + 48u + 16u * c));
         return r;
     }
     __device__ static W load(WPtr w, size_t unit) {
@@ -860,7 +861,14 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
             row = row < a.n ? row : a.n - 1;
             const size_t ru = (size_t)row * (uint32_t)units;   // uniform
 #pragma unroll
-            for (int i = 0; i < BPL; ++i) w[i][r] = F::load_row(a.w, ru, (uint32_t)uu[i]);
+            for (int i = 0; i < BPL; ++i) {
+                uint32_t u = (uint32_t)uu[i];
+                // long rows: the lane offsets are rebuilt per group from u (the
+                // compiler would otherwise hold a 64-bit offset per load across
+                // the group loop, and spill them)
+                if constexpr (BPL >= 5) asm volatile("" : "+v"(u));
+                w[i][r] = F::load_row(a.w, ru, u);
+            }
         }
     };
     const bool has = wave < groups;
@@ -1256,7 +1264,10 @@ __device__ void stage_x16(const void *__restrict__ xin, uint32_t k, uint32_t nt,
 // once per CU at 16 wavefronts per CU) where the body fits 128 VGPRs, else 512.
 template <class F, int BPL>
 constexpr int lds_max_threads() {
-    return (BPL == 1 || (BPL == 2 && (std::is_same<F, FQ4_0>::value || std::is_same<F, FF16>::value))) ? 1024 : 512;
+    return ((BPL == 1 && !std::is_same<F, FQ5_K>::value) ||
+            (BPL == 2 && (std::is_same<F, FQ4_0>::value || std::is_same<F, FF16>::value)))
+               ? 1024
+               : 512;
 }
 
 // LDS-staged variant for binary16 products: workgroups of 512 or 1024

@@ -94,6 +94,7 @@ struct janus_weight {
     void *t32 = nullptr;
     const uint8_t *t32_qs = nullptr;
     const uint8_t *t32_side = nullptr;
+    const uint32_t *t32_q5h = nullptr;   // Q5_K: the fifth bits, one word per lane and chunk
     uint32_t t32_chunks = 0;
 };
 

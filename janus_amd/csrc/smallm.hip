@@ -18,6 +18,10 @@
 //     natural pair (e_2t, e_2t+1) as binary16 1024 + q.
 //     Q4_0 side data: [g][c][32] u32 = the two blocks' binary16 scales.
 //     Q4_K side data: [g][super-block][32] 16-byte headers (d, dmin, scales).
+//   Q5_K: as Q4_K (nibbles and headers), plus the fifth bits: one word per
+//     lane and chunk [g][c][64], bit 4 * slot + i for the element in nibble
+//     slot `slot` of the lane's word i (176 bytes per 256 weights, the GGUF
+//     size).
 //   Q8_0: chunk = 32 K (one block): bytes of elements 8h..8h+7 then
 //     16+8h..16+8h+7; side data [g][c][32] binary16 scales.
 //   F16: chunk = 16 K: the eight binary16 weights 8h..8h+7 of the chunk.
@@ -66,6 +70,25 @@ __device__ __forceinline__ h8 unpack_nib8(uint32_t u, _Float16 off) {
     return (h8){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
+// unpack_nib8 with off = 1024 for 5-bit values: the fifth bits of the word's
+// 8 elements (Q5_K layout above, word I of the lane) are OR-ed into the
+// binary16 mantissas: bit 4 of 1024 + q (slots 0/4, 2/6) or bit 8 of
+// 1024 + 16 q (slots 1/5, 3/7), so the values are q in 0..31, exact.
+template <int I>
+__device__ __forceinline__ h8 unpack_nib8_q5(uint32_t u, uint32_t fifth) {
+    const jh2 o = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const jh2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const jh2 c = {(_Float16)-64.0f, (_Float16)-64.0f};
+    const uint32_t m = vgpr_const_6400();
+    const uint32_t u8 = u >> 8;
+    const uint32_t ta = fifth << (4 - I), tb = fifth >> (4 + I);   // slot s of word I -> bit 4 s + 4, 4 s - 4
+    const jh2 p0 = as_h2((u & 0x000f000fu) | m | (ta & 0x00100010u)) - o;
+    const jh2 p1 = __builtin_elementwise_fma(as_h2((u & 0x00f000f0u) | m | (ta & 0x01000100u)), s16, c);
+    const jh2 p2 = as_h2((u8 & 0x000f000fu) | m | (tb & 0x00100010u)) - o;
+    const jh2 p3 = __builtin_elementwise_fma(as_h2((u8 & 0x00f000f0u) | m | (tb & 0x01000100u)), s16, c);
+    return (h8){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
 // 8 int8 (two words) -> 8 binary16 integers, natural order.
 __device__ __forceinline__ h8 unpack_i8x8(uint32_t lo, uint32_t hi) {
     const jh2 o = {(_Float16)1152.0f, (_Float16)1152.0f};
@@ -88,6 +111,7 @@ __device__ __forceinline__ h8 lds_h8(const _Float16 *p) { return *(const h8 *)p;
 struct GemmArgs {
     const uint8_t *qs;     // T32 quant chunks [G][C][64][16 B]
     const uint8_t *side;   // T32 side data (scales / headers)
+    const uint32_t *q5h;   // Q5_K fifth bits [G][C][64]
     const _Float16 *a;     // activations [rows][k]
     void *c;               // output [rows][n]
     const float *resid;    // [rows][n] or null (may alias c)
@@ -231,41 +255,49 @@ struct GQ4_K {
     }
 };
 
-// Q5_K (GGML block_q5_K): the T32 copy holds each 5-bit value as a byte in
-// the Q8_0 chunk order and, per (row, 32-element sub-block), the pair
-// (d*sc, dmin*m) in binary32; w = (d*sc)*q - dmin*m as for Q4_K, the m term
-// from the staged activation sums.
+// Q5_K (GGML block_q5_K): the Q4_K tiles (nibbles, 16-byte headers) plus the
+// fifth bits of the lane's 32 elements in one word per chunk; w = (d*sc)*q -
+// dmin*m with q in 0..31, the m term from the staged activation sums.
 struct GQ5_K {
-    static constexpr int CK = 32;
-    struct W { uint4 q; float2 s; };
+    static constexpr int CK = 64;
+    struct W { uint4 q; uint4 hdr; uint32_t fifth; };
     __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
         const size_t ch = (size_t)g * a.chunks + c;
         W w;
         w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
-        w.s = ((const float2 *)a.side)[ch * 32 + (lane & 31)];
+        w.fifth = __builtin_nontemporal_load(a.q5h + ch * 64 + lane);
+        const size_t sb = (size_t)g * (a.chunks / 4) + c / 4;
+        w.hdr = *(const uint4 *)(a.side + (sb * 32 + (lane & 31)) * 16);
         return w;
     }
     template <int MT>
     __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
-                               const float *Ss, uint32_t, f16x (&acc)[MT]) {
+                               const float *Ss, uint32_t sub0, f16x (&acc)[MT]) {
         const int h = lane >> 5, r = lane & 31;
-        const h8 b0 = unpack_i8x8(w.q.x, w.q.y);
-        const h8 b1 = unpack_i8x8(w.q.z, w.q.w);
-        const float ds = w.s.x, dm = w.s.y;
-        const uint32_t sub = kl / 32;   // sub-block index within the pass
+        const float d = h2f((uint16_t)(w.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(w.hdr.x >> 16));
+        const int j = (int)((kl / 64 + sub0 / 2) & 3);   // chunk index within the super-block
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + 8 * h;
-            f16x t = mfma(lds_h8(ap), b0, (f16x){});
-            t = mfma(lds_h8(ap + 16), b1, t);
-            const float *sx = Ss + (size_t)sub * (MT * 32) + mt * 32 + 4 * h;
+        for (int b = 0; b < 2; ++b) {
+            float sc, mn;
+            GQ4_K::scale_min(w.hdr, 2 * j + b, sc, mn);
+            const float ds = d * sc, dm = dmin * mn;
+            const h8 b0 = b == 0 ? unpack_nib8_q5<0>(w.q.x, w.fifth) : unpack_nib8_q5<2>(w.q.z, w.fifth);
+            const h8 b1 = b == 0 ? unpack_nib8_q5<1>(w.q.y, w.fifth) : unpack_nib8_q5<3>(w.q.w, w.fifth);
+            const uint32_t sub = kl / 32 + b;   // sub-block index within the pass
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const jf4 s4 = *(const jf4 *)(sx + 8 * jj);
-                acc[mt][4 * jj + 0] = fmaf(-dm, s4.x, fmaf(ds, t[4 * jj + 0], acc[mt][4 * jj + 0]));
-                acc[mt][4 * jj + 1] = fmaf(-dm, s4.y, fmaf(ds, t[4 * jj + 1], acc[mt][4 * jj + 1]));
-                acc[mt][4 * jj + 2] = fmaf(-dm, s4.z, fmaf(ds, t[4 * jj + 2], acc[mt][4 * jj + 2]));
-                acc[mt][4 * jj + 3] = fmaf(-dm, s4.w, fmaf(ds, t[4 * jj + 3], acc[mt][4 * jj + 3]));
+            for (int mt = 0; mt < MT; ++mt) {
+                const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + b * 32 + 8 * h;
+                f16x t = mfma(lds_h8(ap), b0, (f16x){});
+                t = mfma(lds_h8(ap + 16), b1, t);
+                const float *sx = Ss + (size_t)sub * (MT * 32) + mt * 32 + 4 * h;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const jf4 s4 = *(const jf4 *)(sx + 8 * jj);
+                    acc[mt][4 * jj + 0] = fmaf(-dm, s4.x, fmaf(ds, t[4 * jj + 0], acc[mt][4 * jj + 0]));
+                    acc[mt][4 * jj + 1] = fmaf(-dm, s4.y, fmaf(ds, t[4 * jj + 1], acc[mt][4 * jj + 1]));
+                    acc[mt][4 * jj + 2] = fmaf(-dm, s4.z, fmaf(ds, t[4 * jj + 2], acc[mt][4 * jj + 2]));
+                    acc[mt][4 * jj + 3] = fmaf(-dm, s4.w, fmaf(ds, t[4 * jj + 3], acc[mt][4 * jj + 3]));
+                }
             }
         }
     }
@@ -719,46 +751,37 @@ __global__ void t32_q4_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq,
     if (lane < 32 && j == 0) *(uint4 *)(dside + (((size_t)g * (C / 4) + sb) * 32 + lane) * 16) = hdr;
 }
 
-__global__ void t32_q5_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq, float2 *dside, uint32_t n,
-                                uint32_t k, uint32_t G, uint32_t C) {
+__global__ void t32_q5_k_kernel(const uint8_t *__restrict__ blocks, uint8_t *dq, uint8_t *dside, uint32_t *dfifth,
+                                uint32_t n, uint32_t k, uint32_t G, uint32_t C) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (size_t)G * C * 64) return;
     const int lane = (int)(t & 63), h = lane >> 5;
     const size_t ch = t >> 6;
     const uint32_t g = (uint32_t)(ch / C), c = (uint32_t)(ch % C);
-    const uint32_t r = g * 32 + (lane & 31), nsb = k / 256, sb = c / 8, sub = c % 8, j = sub / 2, hb = sub % 2;
-    uint8_t out[16] = {0};
-    float2 side = make_float2(0.0f, 0.0f);
+    const uint32_t r = g * 32 + (lane & 31), nsb = k / 256, sb = c / 4, j = c % 4;
+    uint32_t words[4] = {0u, 0u, 0u, 0u}, fifth = 0u;
+    uint4 hdr = {0u, 0u, 0u, 0u};
     if (r < n) {
         const uint8_t *blk = blocks + ((size_t)r * nsb + sb) * 176, *qs = blk + 48;
-        const uint32_t *qh = (const uint32_t *)(blk + 16);   // one word per 16-byte quant chunk
-        // element e of sub-block 2j + hb: nibble hb of qs[32j + e], its fifth bit
-        // in the word of chunk 2j + e / 16 at bit 8 (t % 4) + t / 4 + 4 hb, t = e % 16
-        auto val = [&](int e) -> uint8_t {
-            const uint32_t q = (qs[32 * j + e] >> (4 * hb)) & 15u;
-            const uint32_t t = (uint32_t)e % 16u, pos = 8 * (t % 4) + t / 4 + 4 * hb;
-            return (uint8_t)(q | (((qh[2 * j + e / 16] >> pos) & 1u) << 4));
-        };
-        for (int e = 0; e < 8; ++e) {
-            out[e] = val(8 * h + e);
-            out[8 + e] = val(16 + 8 * h + e);
+        // the upload's fifth-bit words: one per 16-byte quant chunk, bit
+        // 8 (t % 4) + t / 4 (+ 4 for the high nibble) for quant byte t
+        const uint32_t *qh = (const uint32_t *)(blk + 16);
+        for (int b = 0; b < 2; ++b) {   // sub-block 2j + b: nibble b of bytes 32j + E
+            for (int w = 0; w < 2; ++w) {
+                const int i = 2 * b + w;
+                words[i] = pack_word([&](int e) { return (uint32_t)(qs[32 * j + 16 * w + 8 * h + e] >> (4 * b)); });
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t tq = (uint32_t)(8 * h + e), pos = 8 * (tq % 4) + tq / 4 + 4 * (uint32_t)b;
+                    const uint32_t bit = (qh[2 * j + w] >> pos) & 1u;
+                    fifth |= bit << (4 * nib_slot(e) + (uint32_t)i);
+                }
+            }
         }
-        const uint8_t *sc = blk + 4;
-        uint32_t scv, mnv;
-        if (sub < 4) {
-            scv = sc[sub] & 63u;
-            mnv = sc[sub + 4] & 63u;
-        } else {
-            scv = (sc[sub + 4] & 15u) | ((sc[sub - 4] >> 6) << 4);
-            mnv = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4);
-        }
-        const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t)(blk[2] | (blk[3] << 8)));
-        side = make_float2(d * (float)scv, dmin * (float)mnv);
+        hdr = *(const uint4 *)blk;
     }
-    uint4 v;
-    std::memcpy(&v, out, 16);
-    *(uint4 *)(dq + t * 16) = v;
-    if (lane < 32) dside[ch * 32 + lane] = side;
+    *(uint4 *)(dq + t * 16) = make_uint4(words[0], words[1], words[2], words[3]);
+    dfifth[t] = fifth;
+    if (lane < 32 && j == 0) *(uint4 *)(dside + (((size_t)g * (C / 4) + sb) * 32 + lane) * 16) = hdr;
 }
 
 __global__ void t32_q8_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc, uint8_t *dq,
@@ -806,8 +829,8 @@ __global__ void t32_f16_kernel(const uint16_t *__restrict__ src, uint8_t *dq, ui
 
 uint32_t chunk_k(int type) {
     switch (type) {
-    case JANUS_DT_Q4_0: case JANUS_DT_Q4_K: return 64;
-    case JANUS_DT_Q8_0: case JANUS_DT_Q5_K: return 32;
+    case JANUS_DT_Q4_0: case JANUS_DT_Q4_K: case JANUS_DT_Q5_K: return 64;
+    case JANUS_DT_Q8_0: return 32;
     default: return 16;
     }
 }
@@ -821,11 +844,12 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
     size_t side = 0;
     if (w->type == JANUS_DT_Q4_0) side = (size_t)G * C * 32 * 4;
     else if (w->type == JANUS_DT_Q8_0) side = (size_t)G * C * 32 * 2;
-    else if (w->type == JANUS_DT_Q4_K) side = (size_t)G * (C / 4) * 32 * 16;
-    else if (w->type == JANUS_DT_Q5_K) side = (size_t)G * C * 32 * 8;
+    else if (w->type == JANUS_DT_Q4_K || w->type == JANUS_DT_Q5_K) side = (size_t)G * (C / 4) * 32 * 16;
+    const size_t fifth = w->type == JANUS_DT_Q5_K ? (size_t)G * C * 64 * 4 : 0;
     void *mem = nullptr;
-    JANUS_HIP_CHECK(ctx, hipMalloc(&mem, qbytes + side + 256));
+    JANUS_HIP_CHECK(ctx, hipMalloc(&mem, qbytes + side + fifth + 256));
     uint8_t *dq = (uint8_t *)mem, *ds = (uint8_t *)mem + qbytes;
+    uint32_t *df = (uint32_t *)((uint8_t *)mem + qbytes + side);
     const size_t threads = (size_t)G * C * 64;
     const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
     switch (w->type) {
@@ -837,7 +861,7 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
         hipLaunchKernelGGL(t32_q4_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, ds, w->n, w->k, G, C);
         break;
     case JANUS_DT_Q5_K:
-        hipLaunchKernelGGL(t32_q5_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, (float2 *)ds, w->n, w->k, G, C);
+        hipLaunchKernelGGL(t32_q5_k_kernel, grid, block, 0, ctx->stream, w->qs, dq, ds, df, w->n, w->k, G, C);
         break;
     case JANUS_DT_Q8_0:
         hipLaunchKernelGGL(t32_q8_0_kernel, grid, block, 0, ctx->stream, w->qs, w->sc, dq, (uint16_t *)ds, w->n,
@@ -857,6 +881,7 @@ int t32_ensure(janus_ctx *ctx, janus_weight *w) {
     w->t32 = mem;
     w->t32_qs = dq;
     w->t32_side = ds;
+    w->t32_q5h = fifth ? df : nullptr;
     w->t32_chunks = C;
     return JANUS_OK;
 }
@@ -979,6 +1004,7 @@ GemmArgs make_args(const janus_weight *w, const void *a, void *c, int c_f16, uin
     std::memset(&g, 0, sizeof(g));
     g.qs = w->t32_qs;
     g.side = w->t32_side;
+    g.q5h = w->t32_q5h;
     g.a = (const _Float16 *)a;
     g.c = c;
     g.resid = residual;
