@@ -383,7 +383,8 @@ def main() -> int:
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs32", "copy", "attn", "c3", "gemm", "kquant"],
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs1pen", "bs32", "copy", "attn", "c3", "gemm",
+                                       "kquant"],
                     default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
     args = ap.parse_args()
@@ -476,6 +477,10 @@ def main() -> int:
     if args.only == "bs32":
         ms32, ctx_sum = decode_bs32(engine, spec, args.steps, args.warmup)
         log(f"bs=32 ragged: {ms32 / args.steps:.3f} ms/step, {32 * args.steps / (ms32 / 1e3):.1f} tok/s")
+        return 0
+    if args.only == "bs1pen":
+        msp, _ = decode_bs1(engine, spec, args.steps, args.warmup, penalty=1.15, trials=1)
+        log(f"bs=1 penalty 1.15: {msp / args.steps:.3f} ms/token")
         return 0
     # the headline: exactly K timed steps after W warmup steps
     ms, toks = decode_bs1(engine, spec, args.steps, args.warmup, trials=1)

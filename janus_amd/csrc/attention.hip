@@ -650,12 +650,10 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     const uint64_t waves = (uint64_t)ctx->num_cus * (uint64_t)ctx->attn_wpc;
     if (kv_f16 && !qh && !ctx->attn_valu && batch >= 2 && batch <= 64) {
         // task mode for ragged batches (nw = 1): pieces of `chunk` positions,
-        // about three per wavefront when every sequence is max_len long (ragged
-        // lengths average less: with fewer pieces the wavefronts that get one
-        // more than the rest set the time; measured on 32 sequences at
-        // U[256, 4096]: 4.31 ms per step against 4.59 ms with two)
+        // about two per wavefront when every sequence is max_len long (three
+        // measured 77 against 74 us on config 4 and no better on config 5)
         uint64_t c = ctx->attn_task ? ctx->attn_task
-                                    : ((uint64_t)max_len * batch * kv_heads + 3 * waves - 1) / (3 * waves);
+                                    : ((uint64_t)max_len * batch * kv_heads + 2 * waves - 1) / (2 * waves);
         c = (c + TP - 1) / TP * TP;
         c = c < 64 ? 64 : (c > 1024 ? 1024 : c);
         *chunk_out = (uint32_t)c;
