@@ -968,7 +968,8 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
         }
         int ridx;
         float s = reduce_wave_rows<R>(acc, lane, ridx);
-        if (R == 2 && a.epi >= EPI_QKV_ROPE) {
+        // the paired-row epilogues only (EPI_ARGMAX rides the per-row store below)
+        if (R == 2 && (a.epi == EPI_QKV_ROPE || a.epi == EPI_SWIGLU)) {
             // both row totals in every lane: lanes < 32 hold row 0, lanes >= 32 row 1
             auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
             const float r0 = __uint_as_float(p[0]), r1 = __uint_as_float(p[1]);
@@ -1488,6 +1489,10 @@ int launch_lds_fmt(janus_ctx *ctx, const GemvArgs &a, bool norm, bool pair, bool
         default: return launch_lds<F, 8, 2>(ctx, a, norm);
         }
     }
+    // F16 rows of 8 units per lane (the LM head): two rows per step halve the
+    // cross-lane reductions per row and double the bytes in flight (the body
+    // fits: 4 VGPRs per unit, double-buffered)
+    if (std::is_same<F, FF16>::value && bpl == 8 && ctx->gemv_f16_rows2) return launch_lds<F, 8, 2>(ctx, a, norm);
     switch (bpl) {
     case 1: return launch_lds<F, 1, 4>(ctx, a, norm);
     case 2: return launch_lds<F, 2, 2>(ctx, a, norm);

@@ -30,6 +30,7 @@ struct janus_ctx {
     uint32_t gemv_wpc = 16;
     uint32_t gemv_lds_wpc = 16;
     uint32_t gemv_lds_threads = 0;   // LDS GEMV workgroup size (0: chosen per launch)
+    bool gemv_f16_rows2 = true;      // F16 rows of 8 units per lane: two rows per step
     // binary16-cache attention scores on MFMA (JANUS_ATTN_KERNEL=valu selects
     // the all-VALU kernel instead, for comparisons).
     bool attn_valu = false;
@@ -40,6 +41,8 @@ struct janus_ctx {
     // small-M quantised GEMMs over several K passes per workgroup use the
     // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
     bool gemm_pipe = true;
+    // small-M GEMM pass length / K split forced for every product (0: planned)
+    uint32_t gemm_kr = 0, gemm_ks = 0;
     // Attention split-K partials; grows on first use and is then reused.
     void *attn_ws = nullptr;
     size_t attn_ws_bytes = 0;

@@ -327,7 +327,16 @@ int janus_create(int hip_device, janus_ctx **out) {
         const int v = std::atoi(k);
         if (v == 512 || v == 1024) ctx->gemv_lds_threads = (uint32_t)v;
     }
+    if (const char *k = std::getenv("JANUS_GEMV_F16_ROWS")) ctx->gemv_f16_rows2 = std::strcmp(k, "1") != 0;
     if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
+    if (const char *k = std::getenv("JANUS_GEMM_KR")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v == 256 || v == 512 || v == 1024) ctx->gemm_kr = (uint32_t)v;
+    }
+    if (const char *k = std::getenv("JANUS_GEMM_KS")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v >= 1 && v <= 64) ctx->gemm_ks = (uint32_t)v;
+    }
     if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 16 && v <= 4096) ctx->attn_task = (uint32_t)v;

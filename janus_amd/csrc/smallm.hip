@@ -896,6 +896,10 @@ template <class F, int MT, int KW = gemm_kw<F, MT>(), int PD = Stage<F>::PD>
 int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials *parts, uint32_t kr_force = 0,
                 uint32_t ks_force = 0) {
     constexpr int SPT1 = 16 / KW;   // kr = 1024 / MT
+    if (!kr_force && !ks_force) {   // context-wide overrides (measurement)
+        kr_force = ctx->gemm_kr;
+        ks_force = ctx->gemm_ks;
+    }
     const uint32_t G = (w->n + 31) / 32;
     const uint32_t tiles = (G + WAVES - 1) / WAVES;
     // K per LDS pass: 1024 (M <= 32) or 512 (M <= 64); products with too few

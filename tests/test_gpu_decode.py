@@ -136,6 +136,41 @@ def test_graph_penalty_decode_matches_eager(engine):
         assert outs[0] == outs[1], nseq
 
 
+@pytest.mark.parametrize("hidden", [1024, 2048, 4096])
+def test_folded_lm_head_two_rows_per_step(engine, hidden):
+    """The greedy choice folded into the F16 LM head at 2, 4 and 8 units per
+    lane, where the LDS kernel takes two rows per wavefront step: the key
+    epilogue is the per-row store, not the paired QKV / SwiGLU one (which
+    would write K/V rows through the head's null cache pointers). Graph
+    decode under both sampler rules against eager steps with the host
+    sampler."""
+    s = synth.make_model(57 + hidden, hidden, hidden // 128, hidden // 512, 512, 1000, 1, synth.Q4_0, 1e-5, 500000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    prompt = _prompt(hidden, 6, s.vocab)
+    for mode, penalty in ((_lib.SAMPLER_ARGMAX, 1.0), (_lib.SAMPLER_PENALTY, 1.15)):
+        outs = []
+        for use_graph in (False, True):
+            m = Model(engine, s, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+            for p_, t in enumerate(prompt):
+                m.forward([t], [p_])
+            last, pos, gen = prompt[-1], len(prompt), []
+            if use_graph:
+                m.set_sampler(mode, penalty)
+                m.graph_begin([last], [pos])
+                m.graph_run(8)
+                gen = m.generated(0)
+            else:
+                for _ in range(8):
+                    m.forward([last], [pos])
+                    lg = m.logits()[0]
+                    last = O.argmax_last(lg) if mode == _lib.SAMPLER_ARGMAX else O.greedy_sample(lg, gen, penalty)
+                    gen.append(last)
+                    pos += 1
+            outs.append(list(gen))
+            m.close()
+        assert outs[0] == outs[1], (hidden, mode, outs)
+
+
 def test_kv_slots_equal_logits(engine, spec):
     prompt = _prompt(61, 9, spec.vocab)
     m = Model(engine, spec, max_seq_len=32, max_batch=4)
