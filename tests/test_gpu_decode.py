@@ -281,10 +281,12 @@ def test_stop_token_generate_drops_batch_keeps(engine):
     m.close()
 
 
-def test_workspace_growth_keeps_captured_step(engine):
+def test_workspace_growth_keeps_captured_step():
     """Capture with fewer sequences than max_batch, grow the GEMM workspace
     with a large standalone product, then replay: the captured step must
-    still give the eager tokens (its workspace was retired, not freed)."""
+    still give the eager tokens (its workspace was retired, not freed). A
+    context of its own, so the workspace starts at this test's sizes."""
+    engine = ops.ComputeEngine(0)
     s = synth.make_model(91, 512, 4, 1, 1024, 1000, 2, synth.Q4_0, 1e-5, 500000.0,
                          embed_type=synth.F16, head_type=synth.F16)
     prompts = [_prompt(92, 6, s.vocab), _prompt(93, 6, s.vocab)]
@@ -315,3 +317,5 @@ def test_workspace_growth_keeps_captured_step(engine):
         m.close()
     assert outs[0] == outs[1]
     assert all(len(g) == 9 for g in outs[0])
+    engine.sync()
+    engine.close()

@@ -48,8 +48,6 @@ def _check_against_f64(y, wf, a16):
 @pytest.mark.parametrize("rows", [2, 7, 32, 33, 64])
 @pytest.mark.parametrize("n,k", [(96, 256), (200, 512), (4096, 4096), (1024, 14336)])
 def test_mfma_gemm_matches_stacked_gemv_and_f64(engine, ggml_type, rows, n, k):
-    if rows in (7, 33) and n == 4096:
-        pytest.skip("covered by the other row counts at this shape")
     raw, w = _weight(engine, ggml_type, n, k, 100 + ggml_type + n)
     a16 = _acts(rows, k, rows + n)
     a = a16.to(DEV)
