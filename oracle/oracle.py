@@ -260,12 +260,21 @@ class OracleModel:
 
     kv_f16=True rounds K and V to binary16 on append (the fp16-KV parity mode);
     otherwise the cache is f32 like the reference's (compute/cache/core.rs:60-88).
+
+    act_f16=True also rounds to binary16 every product input that the build's
+    binary16-activation decode path holds in binary16: the attention RMSNorm
+    output, the attention output, the FFN RMSNorm output, the SwiGLU output
+    and the final RMSNorm output (the residual stream, q and the logits stay
+    f32). The reference keeps these in f32; this mode separates the build's
+    storage choice from its arithmetic, so a step whose logits are sensitive
+    to activation rounding is compared with the same rounding applied.
     """
 
-    def __init__(self, spec, max_seq_len: int = 256, kv_f16: bool = False):
+    def __init__(self, spec, max_seq_len: int = 256, kv_f16: bool = False, act_f16: bool = False):
         self.spec = spec
         self.max_seq_len = max_seq_len
         self.kv_f16 = kv_f16
+        self.act_f16 = act_f16
         self.t = {t.name: t for t in spec.tensors}
         self.table = rope_table(max_seq_len, spec.head_dim, spec.rope_theta)
         emb = self.t["token_embd.weight"]
@@ -291,10 +300,11 @@ class OracleModel:
             raise IndexError("token id exceeds vocab")
         if pos >= self.max_seq_len:
             raise IndexError("KV cache position exceeds max_seq_len")
+        h16 = (lambda a: a.astype(np.float16).astype(np.float32)) if self.act_f16 else (lambda a: a)
         x = f16_to_f32(self.embed_bits[token], "ftz")                        # embed.wgsl
         for l in range(s.layers):
             p = f"blk.{l}."
-            xn = rmsnorm(x, self._vec(p + "attn_norm.weight"), s.rms_eps)
+            xn = h16(rmsnorm(x, self._vec(p + "attn_norm.weight"), s.rms_eps))
             q = self._mm(p + "attn_q.weight", xn)
             k = self._mm(p + "attn_k.weight", xn)
             v = self._mm(p + "attn_v.weight", xn)
@@ -305,14 +315,14 @@ class OracleModel:
                 v = v.astype(np.float16).astype(np.float32)
             self.k[l, pos] = k
             self.v[l, pos] = v
-            att = attention(q, self.k[l, : pos + 1], self.v[l, : pos + 1], s.heads, s.kv_heads, s.head_dim)
+            att = h16(attention(q, self.k[l, : pos + 1], self.v[l, : pos + 1], s.heads, s.kv_heads, s.head_dim))
             h1 = add(x, self._mm(p + "attn_output.weight", att))
-            fn = rmsnorm(h1, self._vec(p + "ffn_norm.weight"), s.rms_eps)
+            fn = h16(rmsnorm(h1, self._vec(p + "ffn_norm.weight"), s.rms_eps))
             g = self._mm(p + "ffn_gate.weight", fn)
             u = self._mm(p + "ffn_up.weight", fn)
-            act = mul(silu(g), u)
+            act = h16(mul(silu(g), u))
             x = add(h1, self._mm(p + "ffn_down.weight", act))
-        xn = rmsnorm(x, self._vec("output_norm.weight"), s.rms_eps)
+        xn = h16(rmsnorm(x, self._vec("output_norm.weight"), s.rms_eps))
         return self._mm("output.weight", xn)
 
     def generate(self, prompt, max_tokens: int, penalty: float = 1.15, return_logits: bool = False,

@@ -156,3 +156,40 @@ def test_model_oracle_generate_refeeds_last_prompt_token():
     for p, t in enumerate(prompt):
         m2.forward(t, p)
     assert np.array_equal(m2.forward(prompt[-1], len(prompt)), logits[0])
+
+
+def test_model_oracle_act_f16_rounds_exactly_the_product_inputs():
+    """act_f16 feeds every product (q/k/v, o, gate/up, down, LM head) a
+    binary16-representable input and leaves the residual stream alone: the
+    default mode feeds f32 values that binary16 does not hold, and with
+    act_f16 off the logits are unchanged by the new flag."""
+    spec = synth.tiny_config1(5)
+    prompt = np.random.default_rng(5).integers(0, spec.vocab, 6)
+
+    def run(act_f16):
+        m = O.OracleModel(spec, 32, kv_f16=True, act_f16=act_f16)
+        seen = []
+        mm = m._mm
+
+        def rec(name, x):
+            seen.append((name, np.array(x, dtype=np.float32)))
+            return mm(name, x)
+
+        m._mm = rec
+        out = [m.forward(int(t), p) for p, t in enumerate(prompt)]
+        return out, seen
+
+    base, _ = run(False)
+    ref = O.OracleModel(spec, 32, kv_f16=True)
+    for p, t in enumerate(prompt):
+        assert np.array_equal(ref.forward(int(t), p), base[p])
+    h, seen16 = run(True)
+    _, seen32 = run(False)
+    names = {n.split(".")[-2] if n.startswith("blk.") else n.split(".")[0] for n, _ in seen16}
+    assert names == {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down", "output"}
+    for name, x in seen16:
+        assert np.array_equal(x, x.astype(np.float16).astype(np.float32)), name
+    assert any(not np.array_equal(x, x.astype(np.float16).astype(np.float32)) for _, x in seen32)
+    # binary16 storage of activations moves the logits by a rounding-sized amount
+    for a, b in zip(base, h):
+        assert 0 < np.max(np.abs(a - b)) <= 1e-2 * np.max(np.abs(a))
