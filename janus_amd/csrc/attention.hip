@@ -38,8 +38,7 @@ struct AttnArgs {
     const int32_t *seq_lens;
     uint32_t batch, heads, kv_heads;
     uint32_t seq_len, max_seq;
-    uint32_t max_len;       // the host's bound on every sequence length (flat split)
-    uint32_t chunk;         // positions per wavefront (flat split: least blocks per wavefront)
+    uint32_t chunk;         // positions per wavefront
     uint32_t nw;            // wavefronts per workgroup
     uint32_t splits;        // S: workgroup splits per sequence
     uint32_t qh_div;        // 0: grid.y = KV head (G query heads each); else grid.y = query head, KV head = y / qh_div
@@ -471,73 +470,46 @@ struct MfmaAttn {
     }
 };
 
-// Flat work split for ragged batches (binary16 caches). The 16-position blocks
-// of every (sequence, KV head) pair, in sequence / KV head / position order,
-// are divided into nearly equal contiguous ranges, one per active wavefront
-// (at least a.chunk blocks each, so a pair meets at most a.splits ranges; no
-// wavefront ends the launch with a whole extra piece while the rest idle).
-// A wavefront walks its range as segments (the part of one pair inside it): a
-// segment holding its whole pair writes the output, the others write
-// (m, l, o) partials at slot (sequence, query head, segment index) for
-// attn_merge_flat_kernel, which finds the same ranges from the same lengths.
-// Sequence lengths are clamped to max_len (the host's plan). batch <= 64.
-struct FlatPlan {
-    uint32_t lenb, nbk, incl;   // lane b: length and blocks of sequence b, inclusive block prefix (x KV heads)
-    uint32_t T, nwe;            // blocks in the launch, active wavefronts
-};
-
-__device__ __forceinline__ FlatPlan flat_plan(const AttnArgs &a, int lane, uint32_t nwave) {
-    FlatPlan f;
-    f.lenb = 0;
-    f.nbk = 0;
-    if ((uint32_t)lane < a.batch) {
-        f.lenb = min(min(a.seq_lens ? (uint32_t)a.seq_lens[lane] : a.seq_len, a.max_seq), a.max_len);
-        f.nbk = f.lenb == 0 ? 1u : (f.lenb + 15) / 16;   // an empty sequence still writes zeros
-    }
-    f.incl = f.nbk * a.kv_heads;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t up = (uint32_t)__shfl_up((int)f.incl, o, 64);
-        if (lane >= o) f.incl += up;
-    }
-    f.T = (uint32_t)__shfl((int)f.incl, 63, 64);
-    const uint32_t cap = f.T / a.chunk;
-    f.nwe = min(nwave, cap ? cap : 1u);
-    return f;
-}
-// First block of wavefront w's range, and the wavefront whose range holds block i.
-__device__ __forceinline__ uint32_t flat_begin(const FlatPlan &f, uint32_t w) {
-    return (uint32_t)(((uint64_t)f.T * w) / f.nwe);
-}
-__device__ __forceinline__ uint32_t flat_owner(const FlatPlan &f, uint32_t i) {
-    return (uint32_t)((((uint64_t)i + 1) * f.nwe - 1) / f.T);
-}
-
+// Work list of (sequence, context piece) x KV head tasks of at most `chunk`
+// positions, enumerated on the device from the length table (ragged batches
+// balance across wavefronts whatever the lengths); a persistent grid of
+// wavefronts walks it. A sequence held by one piece writes its output; the
+// others write (m, l, o) partials for attn_merge_kernel. Requires batch <= 64.
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_task_kernel(AttnArgs a) {
     using A = MfmaAttn<D, G>;
     __shared__ float parea[4 * A::PW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float *Pw = parea + wave * A::PW;
-    const FlatPlan f = flat_plan(a, lane, gridDim.x * 4);
-    const uint32_t w = blockIdx.x * 4 + wave;
-    if (w >= f.nwe) return;
-    const uint32_t i1 = flat_begin(f, w + 1);
-    for (uint32_t i = flat_begin(f, w); i < i1;) {
-        // the pair holding block i: sequences whose blocks all precede it, then the KV head
-        const uint64_t le = __ballot(f.incl <= i);
+    const uint32_t C = a.chunk;
+    const uint32_t cap = a.splits * C;
+    // lane b: pieces of sequence b (at least one, so an empty sequence writes zeros)
+    uint32_t lenb = 0, nb = 0;
+    if ((uint32_t)lane < a.batch) {
+        lenb = min(min(a.seq_lens ? (uint32_t)a.seq_lens[lane] : a.seq_len, a.max_seq), cap);
+        nb = lenb == 0 ? 1u : (lenb + C - 1) / C;
+    }
+    uint32_t incl = nb;   // inclusive prefix over lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t up = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += up;
+    }
+    const uint32_t pieces = (uint32_t)__shfl((int)incl, 63, 64);
+    const uint32_t ntask = pieces * a.kv_heads;
+    const uint32_t nwave = gridDim.x * 4;
+    for (uint32_t t = blockIdx.x * 4 + wave; t < ntask; t += nwave) {
+        const uint32_t q = t / a.kv_heads, kvh = t % a.kv_heads;
+        // sequence: the number of lanes whose inclusive prefix is <= q
+        const uint64_t le = __ballot(incl <= q);
         const uint32_t b = (uint32_t)__popcll(le);
-        const uint32_t nb = (uint32_t)__shfl((int)f.nbk, (int)b, 64);
-        const uint32_t excl = (uint32_t)__shfl((int)(f.incl - f.nbk * a.kv_heads), (int)b, 64);
-        const uint32_t len = (uint32_t)__shfl((int)f.lenb, (int)b, 64);
-        const uint32_t kvh = (i - excl) / nb;
-        const uint32_t first = excl + kvh * nb, last = first + nb;   // the pair's blocks [first, last)
-        const uint32_t seg_end = min(i1, last);
-        const uint32_t start = (i - first) * 16, end = min(len, (seg_end - first) * 16);
+        const uint32_t excl = (uint32_t)__shfl((int)(incl - nb), (int)b, 64);
+        const uint32_t len = (uint32_t)__shfl((int)lenb, (int)b, 64);
+        const uint32_t nseq = (uint32_t)__shfl((int)nb, (int)b, 64);
+        const uint32_t j = q - excl;
+        const uint32_t start = j * C, end = min(len, start + C);
         float m, l, acc[G][8];
         A::run(a, b, kvh, start, end, Pw, m, l, acc);
-        const bool whole = i == first && seg_end == last;
-        const uint32_t seg = w - flat_owner(f, first);
         // every lane: (m, l) of head lane & 15; slot-0 lanes: acc of dims 8 * dl
         const int dl = lane % A::LPP;
         const bool writer = lane < A::LPP;
@@ -546,65 +518,19 @@ __global__ __launch_bounds__(256) void attn_task_kernel(AttnArgs a) {
             const float mg = __shfl(m, g, 64), lg = __shfl(l, g, 64);
             const uint32_t h = kvh * G + g;
             if (!writer) continue;
-            if (whole) {
+            if (nseq == 1) {
                 const float inv = 1.0f / fmaxf(lg, 1e-20f);
                 const size_t at = ((size_t)b * a.heads + h) * D + 8 * dl;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) put_out(a, at + k, acc[g][k] * inv);
+                for (int i = 0; i < 8; ++i) put_out(a, at + i, acc[g][i] * inv);
             } else {
-                float *ws = a.ws + (((size_t)b * a.heads + h) * a.splits + seg) * (D + 2);
-                if (dl == 0) { ws[0] = mg; ws[1] = lg; }
+                float *w = a.ws + (((size_t)b * a.heads + h) * a.splits + j) * (D + 2);
+                if (dl == 0) { w[0] = mg; w[1] = lg; }
 #pragma unroll
-                for (int k = 0; k < 8; ++k) ws[2 + 8 * dl + k] = acc[g][k];
+                for (int i = 0; i < 8; ++i) w[2 + 8 * dl + i] = acc[g][i];
             }
         }
-        i = seg_end;
     }
-}
-
-// Merge of the flat split: the segments of (sequence b, query head h) are the
-// ranges of attn_task_kernel that meet its pair; a pair inside one range was
-// written directly. Same log-sum-exp pass as attn_merge_kernel.
-template <int D>
-__global__ __launch_bounds__(D) void attn_merge_flat_kernel(AttnArgs a, uint32_t nwave) {
-    constexpr int SB = 8;
-    const uint32_t h = blockIdx.x, b = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const FlatPlan f = flat_plan(a, lane, nwave);
-    const uint32_t G = a.heads / a.kv_heads, kvh = h / G;
-    const uint32_t nb = (uint32_t)__shfl((int)f.nbk, (int)b, 64);
-    const uint32_t excl = (uint32_t)__shfl((int)(f.incl - f.nbk * a.kv_heads), (int)b, 64);
-    const uint32_t first = excl + kvh * nb;
-    const uint32_t ns = flat_owner(f, first + nb - 1) - flat_owner(f, first) + 1;
-    if (ns <= 1) return;
-    const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);
-    float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (uint32_t s0 = 0; s0 < ns; s0 += SB) {
-        float ms[SB], ls[SB], os[SB];
-#pragma unroll
-        for (int j = 0; j < SB; ++j) {
-            const bool in = s0 + j < ns;
-            const float *ws = w + (size_t)(in ? s0 + j : s0) * (D + 2);
-            ms[j] = in ? ws[0] : -INFINITY;
-            ls[j] = in ? ws[1] : 0.0f;
-            os[j] = in ? ws[2 + threadIdx.x] : 0.0f;
-        }
-        float Mn = M;
-#pragma unroll
-        for (int j = 0; j < SB; ++j) Mn = fmaxf(Mn, ms[j]);
-        if (Mn == -INFINITY) continue;   // no live segment yet
-        const float r = fexp2(M - Mn);
-        L *= r;
-        o *= r;
-#pragma unroll
-        for (int j = 0; j < SB; ++j) {
-            const float e = fexp2(ms[j] - Mn);   // 0 for padding (m = -inf)
-            L = fmaf(ls[j], e, L);
-            o = fmaf(os[j], e, o);
-        }
-        M = Mn;
-    }
-    put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
 }
 
 // Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}, in one pass over
@@ -675,8 +601,7 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
         }
         JANUS_LAUNCH_CHECK(ctx);
         if (a.splits > 1) {
-            hipLaunchKernelGGL((attn_merge_flat_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a,
-                               tgrid.x * 4);
+            hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
             JANUS_LAUNCH_CHECK(ctx);
         }
         return JANUS_OK;
@@ -724,15 +649,16 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     *qh_div_out = qh ? G : 0;
     const uint64_t waves = (uint64_t)ctx->num_cus * (uint64_t)ctx->attn_wpc;
     if (kv_f16 && !qh && !ctx->attn_valu && batch >= 2 && batch <= 64) {
-        // flat split for ragged batches (nw = 1): every active wavefront gets
-        // an equal range of 16-position blocks, at least `chunk` of them
-        // (JANUS_ATTN_TASK sets it in positions), so a pair meets at most
-        // ceil(blocks / chunk) + 1 ranges: the partial slots per (sequence, head)
-        const uint64_t c = ctx->attn_task ? (ctx->attn_task + TP - 1) / TP : 8;
-        const uint64_t nblk = (max_len + TP - 1) / TP;
+        // task mode for ragged batches (nw = 1): pieces of `chunk` positions,
+        // about two per wavefront when every sequence is max_len long (three
+        // measured 77 against 74 us on config 4 and no better on config 5)
+        uint64_t c = ctx->attn_task ? ctx->attn_task
+                                    : ((uint64_t)max_len * batch * kv_heads + 2 * waves - 1) / (2 * waves);
+        c = (c + TP - 1) / TP * TP;
+        c = c < 64 ? 64 : (c > 1024 ? 1024 : c);
         *chunk_out = (uint32_t)c;
         *nw_out = 1;
-        *splits_out = (uint32_t)((nblk + c - 1) / c + 1);
+        *splits_out = (uint32_t)((max_len + c - 1) / c);
         return;
     }
     const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
@@ -805,7 +731,6 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.out_f16 = out_f16;
     uint32_t chunk, nw, splits, qh;
     attention_plan(ctx, batch, heads, kv_heads, max_len, kv_dt == JANUS_DT_F16, &chunk, &nw, &splits, &qh);
-    a.max_len = max_len ? max_len : 1;
     a.chunk = chunk;
     a.nw = nw;
     a.qh_div = qh;
