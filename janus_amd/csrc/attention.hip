@@ -18,6 +18,7 @@
 //    directly.
 //  * Ragged batches: per-sequence row offsets and lengths are device tables,
 //    so all sequences share one launch.
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -28,6 +29,12 @@ namespace janus {
 namespace {
 
 constexpr int TP = 16;        // split granularity in positions
+constexpr uint32_t kRowsMinBlocks = 8;   // row streaming: least 16-position blocks per workgroup
+
+// Row streaming's split partials: [workgroup][2 slots][head][hd + 2] floats.
+size_t rows_partial_bytes(const janus_ctx *ctx, uint32_t heads, uint32_t hd) {
+    return (size_t)ctx->num_cus * 2 * heads * (hd + 2) * sizeof(float);
+}
 
 struct AttnArgs {
     const float *q;
@@ -38,10 +45,12 @@ struct AttnArgs {
     const int32_t *seq_lens;
     uint32_t batch, heads, kv_heads;
     uint32_t seq_len, max_seq;
+    uint32_t max_len;       // longest sequence the plan covers (row streaming clamps lengths to it)
     uint32_t chunk;         // positions per wavefront
     uint32_t nw;            // wavefronts per workgroup
     uint32_t splits;        // S: workgroup splits per sequence
     uint32_t qh_div;        // 0: grid.y = KV head (G query heads each); else grid.y = query head, KV head = y / qh_div
+    uint32_t rows;          // 1: row-streaming kernel (chunk = least 16-position blocks per workgroup)
     float scale;
     float scale2;           // scale * log2(e): the softmax runs in the base-2 domain
     int out_f16;
@@ -533,6 +542,418 @@ __global__ __launch_bounds__(256) void attn_task_kernel(AttnArgs a) {
     }
 }
 
+// Row-streaming attention for ragged batches (binary16 caches, D = 128, 4 or
+// 8 KV heads): one workgroup of KVH wavefronts (wavefront w = KV head w) per
+// CU. A cache row holds every KV head of a position (the reference layout
+// [position][kv_head][dim]), so a workgroup that serves all KV heads reads
+// whole contiguous rows: per 16-position block its wavefronts copy 16 K rows
+// and 16 V rows straight into LDS (LDS-DMA loads, 1 KB each, rows padded by 16
+// bytes so the MFMA operand reads hit every bank), double buffered across
+// blocks and sequences, and each wavefront runs the block step of MfmaAttn
+// for its KV head from LDS (scores on MFMA, online softmax, P.V on the VALU).
+// Work split: the blocks of all sequences, in order, are divided into equal
+// contiguous ranges, one per active workgroup (at least a.chunk blocks each);
+// a sequence spread over several ranges writes one (m, l, o) partial per
+// range for attn_merge_rows_kernel. Lengths are clamped to max_len. batch <= 64.
+constexpr int RBP = 16;   // positions per block
+
+struct RowsPlan {
+    uint32_t lenb, nbk, incl, rowb;   // lane b: length, blocks, inclusive block prefix, first cache row
+    uint32_t T, nwg;                  // blocks in the launch, active workgroups
+};
+
+__device__ __forceinline__ RowsPlan rows_plan(const AttnArgs &a, int lane, uint32_t nwg_grid) {
+    RowsPlan f;
+    f.lenb = 0;
+    f.nbk = 0;
+    f.rowb = 0;
+    if ((uint32_t)lane < a.batch) {
+        f.lenb = min(min(a.seq_lens ? (uint32_t)a.seq_lens[lane] : a.seq_len, a.max_seq), a.max_len);
+        f.nbk = f.lenb == 0 ? 1u : (f.lenb + RBP - 1) / RBP;   // an empty sequence still writes zeros
+        f.rowb = a.row_base ? (uint32_t)a.row_base[lane] : (uint32_t)lane * a.max_seq;
+    }
+    f.incl = f.nbk;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t up = (uint32_t)__shfl_up((int)f.incl, o, 64);
+        if (lane >= o) f.incl += up;
+    }
+    f.T = (uint32_t)__shfl((int)f.incl, 63, 64);
+    const uint32_t cap = f.T / a.chunk;
+    f.nwg = min(nwg_grid, cap ? cap : 1u);
+    return f;
+}
+// floor(T * w / nwg) and the workgroup that holds block i. The products are
+// below 2^53 and the divisors below 2^32, so correctly rounded double
+// division followed by truncation is the exact integer quotient (a quotient
+// that is not an integer is at least 1 / divisor away from one).
+__device__ __forceinline__ uint32_t rows_begin(const RowsPlan &f, uint32_t w) {
+    return (uint32_t)((double)((uint64_t)f.T * w) / (double)f.nwg);
+}
+__device__ __forceinline__ uint32_t rows_owner(const RowsPlan &f, uint32_t i) {
+    return (uint32_t)((double)(((uint64_t)i + 1) * f.nwg - 1) / (double)f.T);
+}
+
+template <int D, int G, int KVH>
+struct RowsLds {
+    static constexpr uint32_t RB = KVH * D * 2;       // bytes of a cache row
+    static constexpr uint32_t RP = RB + 16;           // LDS row pitch
+    static constexpr uint32_t TILE = RBP * RP;        // 16 rows
+    static constexpr uint32_t BUF = 2 * TILE;         // K and V tiles of a block
+    static constexpr uint32_t NDMA = RBP / KVH * (RB / 1024) * 2;   // 1 KB requests per wavefront per block
+    static constexpr uint32_t QW = G * D * 4;         // q of a wavefront's G heads (fp32)
+    static constexpr uint32_t NQ = (QW + 1023) / 1024;   // requests for it
+    static constexpr uint32_t PW = RBP * G + G;       // floats of a wavefront's P area
+    static constexpr uint32_t BYTES = 2 * BUF + KVH * QW + KVH * PW * 4;
+};
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (non-temporal; lds is wavefront-uniform and goes to M0). Issued as inline
+// assembly so that the compiler tracks none of these requests: every wait for
+// them is an explicit vmcnt wait below. M0 is not named as clobbered (the
+// compiler reserves it); the kernels that call this make no other use of M0.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// s_waitcnt vmcnt(N), other counters unconstrained (gfx9 encoding)
+template <uint32_t N> __device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int D, int G, int KVH>
+__global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
+    using L = RowsLds<D, G, KVH>;
+    constexpr int KS = D / 32, LPP = D / 8, SLOTS = 64 / LPP, STEPS = RBP / SLOTS;
+    static_assert(D == 128 && (KVH == 4 || KVH == 8) && L::NDMA == 8 && G <= 8, "row streaming: D 128, 4 or 8 KV heads");
+    static_assert(L::BYTES <= 160 * 1024, "row streaming: LDS");
+    __shared__ __align__(16) unsigned char lds[L::BYTES];
+    const int lane = threadIdx.x & 63;
+    const uint32_t kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    unsigned char *qw = lds + 2 * L::BUF + kvh * L::QW;                        // this wavefront's q
+    float *Pw = (float *)(lds + 2 * L::BUF + KVH * L::QW) + kvh * L::PW;      // and P area
+    const int slot = lane / LPP, dl = lane % LPP;   // P.V layout
+    const int col = lane & 15, grp = lane >> 4;     // MFMA layout
+    const RowsPlan f = rows_plan(a, lane, gridDim.x);
+    const uint32_t w = blockIdx.x;
+    if (w >= f.nwg) return;
+    const uint32_t i0 = rows_begin(f, w), i1 = rows_begin(f, w + 1);
+    const uint32_t kvrow = KVH * D;
+
+    struct Blk { uint32_t b, j, nb, len, first; };
+    auto locate = [&](uint32_t i) {
+        Blk k;
+        const uint64_t le = __ballot(f.incl <= i);   // sequences that end before block i
+        k.b = (uint32_t)__popcll(le);
+        k.nb = (uint32_t)__shfl((int)f.nbk, (int)k.b, 64);
+        k.first = (uint32_t)__shfl((int)(f.incl - f.nbk), (int)k.b, 64);
+        k.len = (uint32_t)__shfl((int)f.lenb, (int)k.b, 64);
+        k.j = i - k.first;
+        return k;
+    };
+    // This wavefront's share of block k's rows (RBP / KVH rows of K and of V)
+    // into buffer buf; returns the number of requests (0 or NDMA).
+    auto issue_rows = [&](int buf, const Blk &k) -> uint32_t {
+        if (!k.len) return 0;
+        const uint32_t rowb = (uint32_t)__shfl((int)f.rowb, (int)k.b, 64);
+        const uint32_t kt = lds_addr(lds) + buf * L::BUF, vt = kt + L::TILE;
+#pragma unroll
+        for (int r = 0; r < RBP / KVH; ++r) {
+            const uint32_t row = kvh * (RBP / KVH) + r;
+            const uint32_t p = min(k.j * RBP + row, k.len - 1);   // rows past the end: masked, stay in the sequence
+            const size_t e = ((size_t)rowb + p) * kvrow + lane * 8;
+#pragma unroll
+            for (uint32_t h = 0; h < L::RB / 1024; ++h) {
+                lds_dma16((const _Float16 *)a.kc + e + h * 512, kt + row * L::RP + h * 1024);
+                lds_dma16((const _Float16 *)a.vc + e + h * 512, vt + row * L::RP + h * 1024);
+            }
+        }
+        return L::NDMA;
+    };
+    // q of the G heads of KV head kvh of sequence b (G * D contiguous floats)
+    // into this wavefront's q area: NQ requests
+    auto issue_q = [&](uint32_t b) {
+        const float *src = a.q + ((size_t)b * a.heads + kvh * G) * D;
+#pragma unroll
+        for (uint32_t c = 0; c < L::NQ; ++c)
+            if (L::QW >= 1024 * (c + 1) || lane * 16 < L::QW - 1024 * c)
+                lds_dma16(src + c * 256 + lane * 4, lds_addr(qw) + c * 1024);
+    };
+
+    ah8 qh[KS], qm[KS], ql[KS];
+    float sc2 = 0.0f;
+    float m = -INFINITY, l = 0.0f, acc[G][8];
+
+    Blk cur = locate(i0);
+    bool cur_start = true;
+    (void)issue_rows(0, cur);
+    issue_q(cur.b);
+    // q requests were made after the current block's rows: the wait for the
+    // rows may leave them pending unless the block starts a segment
+    bool q_newer = true;
+    uint32_t i = i0;
+    // One block: request block i + 1 into the other buffer, wait for block i,
+    // run it. BUF is the buffer of block i.
+    auto step = [&](auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        const bool cur_end = i + 1 == i1 || cur.j + 1 == cur.nb;
+        Blk nxt = cur;
+        bool nxt_start = false;
+        uint32_t nn = 0;
+        if (i + 1 < i1) {
+            nxt = locate(i + 1);
+            nxt_start = cur_end;
+            nn = issue_rows(buf ^ 1, nxt);
+        }
+        // requests complete in order: block i's rows (and q when the block
+        // starts a segment) are older than the newest nn (+ NQ) requests
+        const bool qp = q_newer && !cur_start;
+        if (nn && qp) wait_vm<L::NDMA + L::NQ>();
+        else if (nn) wait_vm<L::NDMA>();
+        else if (qp) wait_vm<L::NQ>();
+        else wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        q_newer = false;
+
+        if (cur_start) {
+            // q of head `col` (zero for col >= G), dims 8*grp + 32t + e
+            float qv[KS][8];
+            float qmax = 0.0f;
+            const float *qs_lds = (const float *)qw + (col < G ? col : 0) * D + 8 * grp;
+#pragma unroll
+            for (int t = 0; t < KS; ++t) {
+                const jf4 q0 = *(const jf4 *)(qs_lds + 32 * t), q1 = *(const jf4 *)(qs_lds + 32 * t + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[t][e] = col < G ? q0[e] : 0.0f;
+                    qv[t][4 + e] = col < G ? q1[e] : 0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(qv[t][e]));
+            }
+            qmax = fmaxf(qmax, lane_xor<16>(qmax));
+            qmax = fmaxf(qmax, lane_xor<32>(qmax));
+            int qe = 0;
+            (void)frexpf(qmax, &qe);                  // qmax < 2^qe
+            const int sh = qe > 15 ? qe - 15 : 0;     // |q| * 2^-sh < 2^15
+            const float qs = ldexpf(1.0f, -sh);
+            sc2 = a.scale2 * ldexpf(1.0f, sh);
+#pragma unroll
+            for (int t = 0; t < KS; ++t)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = qv[t][e] * qs;
+                    const _Float16 hi = (_Float16)x;
+                    const float r = x - (float)hi;
+                    const _Float16 mid = (_Float16)r;
+                    qh[t][e] = hi;
+                    qm[t][e] = mid;
+                    ql[t][e] = (_Float16)(r - (float)mid);
+                }
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+            m = -INFINITY;
+            l = 0.0f;
+            // q of the next sequence, when its first block is in this range;
+            // the q area is rewritten only after this wavefront's reads of it
+            if (cur.first + cur.nb < i1) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue_q(cur.b + 1);
+                q_newer = true;
+            }
+        }
+
+        // ---- the block step for KV head kvh, K and V from LDS ----
+        const unsigned char *kt = lds + buf * L::BUF, *vt = kt + L::TILE;
+        const uint32_t p0 = cur.j * RBP, end = cur.len;
+        if (p0 < end) {
+            af4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < KS; ++t) {
+                const ah8 kk = __builtin_bit_cast(
+                    ah8, *(const uint4 *)(kt + col * L::RP + kvh * D * 2 + (8 * grp + 32 * t) * 2));
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, ql[t], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qm[t], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[t], S, 0, 0, 0);
+            }
+            // S[r]: head col, position p0 + 4*grp + r
+            float sv[4];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool live = p0 + 4 * grp + r < end;
+                sv[r] = live ? S[r] * sc2 : -INFINITY;
+                bm = fmaxf(bm, sv[r]);
+            }
+            bm = fmaxf(bm, lane_xor<16>(bm));
+            bm = fmaxf(bm, lane_xor<32>(bm));
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fexp2(m - mn);
+            float ps[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ps[r] = mn == -INFINITY ? 0.0f : fexp2(sv[r] - mn);
+            l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+            m = mn;
+            if (col < G) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Pw[(4 * grp + r) * G + col] = ps[r];
+                if (grp == 0) Pw[RBP * G + col] = alpha;
+            }
+            // the area is read by other lanes of this wavefront only: LDS
+            // operations of one wavefront complete in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float al = Pw[RBP * G + g];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] *= al;
+            }
+#pragma unroll
+            for (int u = 0; u < STEPS; ++u) {
+                const float *pr = Pw + (u * SLOTS + slot) * G;
+                KVRow<_Float16> vrow;
+                vrow.r = *(const uint4 *)(vt + (u * SLOTS + slot) * L::RP + kvh * D * 2 + 16 * dl);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float pg = pr[g];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg, vrow.get(e), acc[g][e]);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+
+        if (cur_end) {
+            // slots share the running maximum: sum acc over slots, l over the 4 position groups
+            // (in place: the next block starts a segment and clears acc)
+            float lt = l + lane_xor<16>(l);
+            lt += lane_xor<32>(lt);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    acc[g][e] += lane_xor<16>(acc[g][e]);
+                    acc[g][e] += lane_xor<32>(acc[g][e]);
+                }
+            // the sequence's blocks all lie in this workgroup's range: write
+            // the output; else a partial in slot 0 (the segment that holds the
+            // range's first block) or slot 1 (the one that runs past its end)
+            const bool whole = rows_owner(f, cur.first) == w && rows_owner(f, cur.first + cur.nb - 1) == w;
+            const uint32_t slot2 = cur.first <= i0 ? 0u : 1u;
+            const bool writer = lane < LPP;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float mg = __shfl(m, g, 64), lg = __shfl(lt, g, 64);
+                const uint32_t h = kvh * G + g;
+                if (writer) {
+                    if (whole) {
+                        const float inv = 1.0f / fmaxf(lg, 1e-20f);
+                        const size_t at0 = ((size_t)cur.b * a.heads + h) * D + 8 * dl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) put_out(a, at0 + e, acc[g][e] * inv);
+                    } else {
+                        float *ws = a.ws + (((size_t)w * 2 + slot2) * a.heads + h) * (D + 2);
+                        if (dl == 0) { ws[0] = mg; ws[1] = lg; }
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ws[2 + 8 * dl + e] = acc[g][e];
+                    }
+                }
+            }
+        }
+        // every wavefront is done with this buffer before it is refilled
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        cur = nxt;
+        cur_start = nxt_start;
+        ++i;
+    };
+    while (i < i1) {
+        step(std::integral_constant<int, 0>{});
+        if (i >= i1) break;
+        step(std::integral_constant<int, 1>{});
+    }
+}
+
+// Merge of the row-streaming split: sequence b's segments are the partials
+// of the workgroups whose ranges meet its blocks ([w][slot][head][D + 2]:
+// slot 0 when the sequence holds the range's first block, else slot 1); a
+// sequence inside one range was written directly. Lane j of each 64-segment
+// chunk reads segment j's (m, l) and weight, so the maxima and sums take one
+// round trip per chunk, and the o loads of a chunk are all independent.
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_rows_kernel(AttnArgs a, uint32_t nwg_grid) {
+    const uint32_t h = blockIdx.x, b = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const RowsPlan f = rows_plan(a, lane, nwg_grid);
+    const uint32_t nb = (uint32_t)__shfl((int)f.nbk, (int)b, 64);
+    const uint32_t first = (uint32_t)__shfl((int)(f.incl - f.nbk), (int)b, 64);
+    const uint32_t w0 = rows_owner(f, first), ns = rows_owner(f, first + nb - 1) - w0 + 1;
+    if (ns <= 1) return;
+    __shared__ float e_s[D / 64][64];
+    __shared__ uint32_t off_s[D / 64][64];
+    const int wv = threadIdx.x >> 6;
+    float M = -INFINITY, L = 0.0f, o = 0.0f;
+    for (uint32_t j0 = 0; j0 < ns; j0 += 64) {
+        const uint32_t j = j0 + lane, cnt = min(ns - j0, 64u);
+        float mj = -INFINITY, lj = 0.0f;
+        uint32_t offj = 0;
+        if (j < ns) {
+            const uint32_t wj = w0 + j;
+            const uint32_t slot = first <= rows_begin(f, wj) ? 0u : 1u;
+            offj = (((uint32_t)wj * 2 + slot) * a.heads + h) * (D + 2);
+            mj = a.ws[offj];
+            lj = a.ws[offj + 1];
+        }
+        float Mc = mj;
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, s, 64));
+        const float Mn = fmaxf(M, Mc);
+        if (Mn == -INFINITY) continue;   // no live segment yet
+        const float r = fexp2(M - Mn);   // 0 while M = -inf
+        const float ej = fexp2(mj - Mn); // 0 for dead segments and idle lanes
+        float ls = lj * ej;
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) ls += __shfl_xor(ls, s, 64);
+        L = L * r + ls;
+        o *= r;
+        // weights and offsets through this wavefront's LDS slots, so the o
+        // loads of 16 segments go out together
+        e_s[wv][lane] = ej;
+        off_s[wv][lane] = offj;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (uint32_t jj = 0; jj < cnt; jj += 16) {
+            float ov[16], ev[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const bool in = jj + k < cnt;
+                const uint32_t q = in ? jj + k : jj;
+                ev[k] = in ? e_s[wv][q] : 0.0f;
+                ov[k] = a.ws[off_s[wv][q] + 2 + threadIdx.x];
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) o = fmaf(ev[k], ov[k], o);
+        }
+        // the slots are rewritten by the next chunk
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        M = Mn;
+    }
+    put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
+}
+
 // Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}, in one pass over
 // the splits with a running maximum; the partials of 8 splits are loaded
 // together, so a merge costs ns / 8 dependent round trips.
@@ -588,6 +1009,28 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
         }
         return JANUS_OK;
     }
+    if constexpr (D == 128 && std::is_same<KV, _Float16>::value) {
+        if (a.rows) {   // row streaming: one workgroup of kv_heads wavefronts per CU
+            const dim3 rgrid(ctx->num_cus);
+#define JANUS_ROWS_CASE(GG, KK)                                                                               \
+    if (G == GG && a.kv_heads == KK) {                                                                        \
+        hipLaunchKernelGGL((attn_rows_kernel<D, GG, KK>), rgrid, dim3(64 * KK), 0, ctx->stream, a);           \
+        found = true;                                                                                         \
+    }
+            bool found = false;
+            JANUS_ROWS_CASE(1, 4) JANUS_ROWS_CASE(2, 4) JANUS_ROWS_CASE(4, 4) JANUS_ROWS_CASE(8, 4)
+            JANUS_ROWS_CASE(1, 8) JANUS_ROWS_CASE(2, 8) JANUS_ROWS_CASE(4, 8)
+#undef JANUS_ROWS_CASE
+            if (!found) return fail(ctx, JANUS_E_INVALID_DIM, "attention: row streaming needs 4 or 8 KV heads, at most 32 heads");
+            JANUS_LAUNCH_CHECK(ctx);
+            if (a.splits > 1) {
+                hipLaunchKernelGGL((attn_merge_rows_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a,
+                                   (uint32_t)ctx->num_cus);
+                JANUS_LAUNCH_CHECK(ctx);
+            }
+            return JANUS_OK;
+        }
+    }
     dim3 grid(a.splits, a.kv_heads, a.batch), block(64 * a.nw);
     const size_t lds = (size_t)a.nw * G * (D + 2) * 4;
     if (std::is_same<KV, _Float16>::value && a.nw == 1) {   // task mode (binary16 caches)
@@ -638,16 +1081,35 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
 // positions use 16-wavefront (G <= 2) or 8-wavefront (G = 4) workgroups whose
 // wavefronts merge in LDS, so short contexts need no merge launch; otherwise
 // 4-wavefront workgroups, with a merge kernel across workgroup splits.
-void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    int kv_f16, uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out, uint32_t *qh_div_out) {
+void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                    uint32_t max_len, int kv_f16, uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out,
+                    uint32_t *qh_div_out, uint32_t *rows_out) {
     if (max_len == 0) max_len = 1;
     const uint32_t G = heads / kv_heads;
+    *rows_out = 0;
     // Short contexts with few sequences: one workgroup per query head (the G
     // heads of a KV head re-read its rows from L2) so the launch spreads over
     // G times more CUs and each wavefront does 1/G of the arithmetic.
     const bool qh = G > 1 && max_len <= 1024 && (uint64_t)batch * heads <= (uint64_t)ctx->num_cus;
     *qh_div_out = qh ? G : 0;
     const uint64_t waves = (uint64_t)ctx->num_cus * (uint64_t)ctx->attn_wpc;
+    // Row streaming (one workgroup per CU over ranges of 16-position blocks):
+    // ragged batches that give every CU's range at least kRowsMinBlocks
+    // blocks when all sequences are max_len long. Partials are kept per
+    // workgroup (two slots), so their size depends on neither batch nor length.
+    const uint64_t nbmax = (max_len + 15) / 16;
+    const bool rows_ok = kv_f16 && !qh && !ctx->attn_valu && batch >= 2 && batch <= 64 && hd == 128 &&
+                         (kv_heads == 4 || kv_heads == 8) && (G == 1 || G == 2 || G == 4 || G == 8) &&
+                         heads == G * kv_heads && heads <= 32 && ctx->num_cus > 0 &&
+                         rows_partial_bytes(ctx, heads, hd) <= kAttnScratchBytes;
+    if (rows_ok && (ctx->attn_rows == 1 ||
+                    (ctx->attn_rows < 0 && batch * nbmax >= (uint64_t)kRowsMinBlocks * ctx->num_cus))) {
+        *rows_out = 1;
+        *chunk_out = kRowsMinBlocks;
+        *nw_out = kv_heads;
+        *splits_out = 2;   // partial slots per workgroup
+        return;
+    }
     if (kv_f16 && !qh && !ctx->attn_valu && batch >= 2 && batch <= 64) {
         // task mode for ragged batches (nw = 1): pieces of `chunk` positions,
         // about two per wavefront when every sequence is max_len long (three
@@ -673,8 +1135,9 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
 
 size_t attention_ws_bytes(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                           uint32_t max_len, int kv_f16) {
-    uint32_t chunk, nw, splits, qh;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, kv_f16, &chunk, &nw, &splits, &qh);
+    uint32_t chunk, nw, splits, qh, rows;
+    attention_plan(ctx, batch, heads, kv_heads, hd, max_len, kv_f16, &chunk, &nw, &splits, &qh, &rows);
+    if (rows) return rows_partial_bytes(ctx, heads, hd);
     if (splits <= 1) return 0;
     return (size_t)batch * heads * splits * (hd + 2) * sizeof(float);
 }
@@ -726,18 +1189,22 @@ int attention_launch(janus_ctx *ctx, const float *q, const void *kc, const void 
     a.kv_heads = kv_heads;
     a.seq_len = seq_len;
     a.max_seq = max_seq;
+    a.max_len = max_len;
     a.scale = scale;
     a.scale2 = scale * 1.4426950408889634f;
     a.out_f16 = out_f16;
-    uint32_t chunk, nw, splits, qh;
-    attention_plan(ctx, batch, heads, kv_heads, max_len, kv_dt == JANUS_DT_F16, &chunk, &nw, &splits, &qh);
+    uint32_t chunk, nw, splits, qh, rows;
+    attention_plan(ctx, batch, heads, kv_heads, hd, max_len, kv_dt == JANUS_DT_F16, &chunk, &nw, &splits, &qh,
+                   &rows);
     a.chunk = chunk;
     a.nw = nw;
     a.qh_div = qh;
+    a.rows = rows;
     a.splits = splits;
     a.ws = nullptr;
     if (splits > 1) {
-        size_t bytes = (size_t)batch * heads * splits * (hd + 2) * sizeof(float);
+        const size_t bytes = rows ? rows_partial_bytes(ctx, heads, hd)
+                                  : (size_t)batch * heads * splits * (hd + 2) * sizeof(float);
         if (fixed_ws) {
             if (bytes > fixed_ws_bytes)
                 return fail(ctx, JANUS_E_INVALID_DIM,

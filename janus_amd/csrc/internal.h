@@ -38,6 +38,10 @@ struct janus_ctx {
     uint32_t attn_wpc = 8;
     // binary16-cache attention piece length in positions (0: planned; JANUS_ATTN_TASK)
     uint32_t attn_task = 0;
+    // ragged binary16-cache batches with 4 or 8 KV heads of 128 dims stream
+    // whole cache rows through LDS, one workgroup per CU (JANUS_ATTN_ROWS:
+    // 0 never, 1 whenever the shape allows, unset: planned)
+    int attn_rows = -1;
     // small-M quantised GEMMs over several K passes per workgroup use the
     // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
     bool gemm_pipe = true;
@@ -201,8 +205,10 @@ int kv_update_launch(janus_ctx *ctx, const float *k_new, const float *v_new, voi
                      uint32_t batch, uint32_t row_elems, uint32_t position, uint32_t max_seq,
                      const int32_t *row_base, const int32_t *positions);
 // Attention split sizing shared by the launch and workspace reservation.
-void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t max_len,
-                    int kv_f16, uint32_t *chunk, uint32_t *nw, uint32_t *splits, uint32_t *qh_div);
+// rows: 1 when the row-streaming kernel runs (chunk then counts 16-position blocks).
+void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+                    uint32_t max_len, int kv_f16, uint32_t *chunk, uint32_t *nw, uint32_t *splits,
+                    uint32_t *qh_div, uint32_t *rows);
 // Bytes of split partials a launch of this shape writes (0: no split).
 size_t attention_ws_bytes(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                           uint32_t max_len, int kv_f16);

@@ -127,3 +127,124 @@ def test_attention_large_q_prescale(engine):
         # overflow of the binary16 q parts would give inf / nan instead
         want = O.attention(q[b], k[sl], v[sl], H, KVH, D)
         assert np.allclose(got[b], want, rtol=1e-4, atol=1e-5), np.max(np.abs(got[b] - want))
+
+
+@pytest.fixture(scope="module")
+def rows_engine():
+    """A context whose planner takes the row-streaming kernel whenever the
+    shape allows it (JANUS_ATTN_ROWS=1 is read when the context is made)."""
+    import os
+    from janus_amd.ops import ComputeEngine
+    old = os.environ.get("JANUS_ATTN_ROWS")
+    os.environ["JANUS_ATTN_ROWS"] = "1"
+    try:
+        eng = ComputeEngine(0)
+    finally:
+        if old is None:
+            del os.environ["JANUS_ATTN_ROWS"]
+        else:
+            os.environ["JANUS_ATTN_ROWS"] = old
+    yield eng
+    eng.sync()
+    eng.close()
+
+
+def _ragged_f16(rng, lens, H, KVH, D, qscale=1.0):
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    total = max(int(sum(lens)), 1)
+    k = rng.standard_normal((total, KVH, D)).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((total, KVH, D)).astype(np.float16).astype(np.float32)
+    q = (rng.standard_normal((len(lens), H * D)) * qscale).astype(np.float32)
+    dev = dict(q=torch.from_numpy(q).to(DEV), kc=torch.from_numpy(k).to(DEV, torch.float16),
+               vc=torch.from_numpy(v).to(DEV, torch.float16), offs=torch.from_numpy(offs).to(DEV),
+               lens=torch.tensor(lens, dtype=torch.int32, device=DEV))
+    return q, k, v, offs, dev
+
+
+def _run_ragged(eng, dev, lens, H, KVH, D):
+    B = len(lens)
+    out = torch.full((B, H * D), 7.0, device=DEV)
+    mx = max(max(lens), 1)
+    ops.compute_attention(eng, dev["q"], dev["kc"], dev["vc"], out, B, 0, mx, H, KVH, D, row_base=dev["offs"],
+                          seq_lens=dev["lens"], max_len_hint=mx)
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("H,KVH,D", [(32, 8, 128), (16, 8, 128), (8, 8, 128), (32, 4, 128), (16, 4, 128),
+                                     (4, 4, 128)])
+def test_attention_rows_ragged_edges(rows_engine, H, KVH, D):
+    """Row streaming (whole cache rows of a 16-position block through LDS,
+    workgroup ranges of blocks across sequences): empty sequences give zeros,
+    and lengths on either side of block and range boundaries match the f64
+    oracle, including sequences split over several workgroups and runs of
+    one-block sequences inside one workgroup."""
+    rng = np.random.default_rng(H * 11 + KVH)
+    lens = [0, 1, 15, 16, 17, 255, 256, 257, 1023, 1025, 2500, 3, 0, 16, 1, 31]
+    q, k, v, offs, dev = _ragged_f16(rng, lens, H, KVH, D)
+    got = _run_ragged(rows_engine, dev, lens, H, KVH, D)
+    for b in range(len(lens)):
+        if lens[b] == 0:
+            assert np.count_nonzero(got[b]) == 0
+            continue
+        sl = slice(offs[b], offs[b] + lens[b])
+        _close(got[b], O.attention(q[b], k[sl], v[sl], H, KVH, D))
+
+
+@pytest.mark.parametrize("lens_kind", ["short64", "mixed64", "two_long"])
+def test_attention_rows_batches(rows_engine, lens_kind):
+    """Row streaming at the batch limits: 64 one-block sequences (every
+    block starts a segment), 64 mixed lengths, and two long sequences (each
+    spread over many workgroups, merged)."""
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng({"short64": 1, "mixed64": 2, "two_long": 3}[lens_kind])
+    if lens_kind == "short64":
+        lens = rng.integers(1, 17, 64).tolist()
+    elif lens_kind == "mixed64":
+        lens = rng.integers(0, 2000, 64).tolist()
+    else:
+        lens = [6000, 4500]
+    q, k, v, offs, dev = _ragged_f16(rng, lens, H, KVH, D)
+    got = _run_ragged(rows_engine, dev, lens, H, KVH, D)
+    for b in range(len(lens)):
+        if lens[b] == 0:
+            assert np.count_nonzero(got[b]) == 0
+            continue
+        sl = slice(offs[b], offs[b] + lens[b])
+        _close(got[b], O.attention(q[b], k[sl], v[sl], H, KVH, D))
+
+
+def test_attention_rows_large_q_prescale(rows_engine):
+    """q beyond the binary16 range through the row-streaming kernel (q is
+    staged through LDS there): power-of-two prescale as in the other kernels."""
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng(19)
+    lens = [40, 300, 17]
+    offs = np.array([0, 40, 340], np.int32)
+    k = (rng.standard_normal((357, KVH, D)) * 2e-5).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((357, KVH, D)).astype(np.float16).astype(np.float32)
+    q = (rng.standard_normal((3, H * D)) * 2e5).astype(np.float32)
+    out = torch.empty(3, H * D, device=DEV)
+    ops.compute_attention(rows_engine, torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV, torch.float16),
+                          torch.from_numpy(v).to(DEV, torch.float16), out, 3, 0, 300, H, KVH, D,
+                          row_base=torch.from_numpy(offs).to(DEV),
+                          seq_lens=torch.tensor(lens, dtype=torch.int32, device=DEV), max_len_hint=300)
+    got = out.cpu().numpy()
+    for b in range(3):
+        sl = slice(offs[b], offs[b] + lens[b])
+        want = O.attention(q[b], k[sl], v[sl], H, KVH, D)
+        assert np.allclose(got[b], want, rtol=1e-4, atol=1e-5), np.max(np.abs(got[b] - want))
+
+
+def test_attention_rows_matches_default_plan_at_config4_shape(engine, rows_engine):
+    """At the 32-sequence benchmark shape the default planner and the forced
+    row-streaming plan agree to fp32 rounding (different split points)."""
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng(32)
+    lens = rng.integers(1024, 4097, 32).tolist()
+    q, k, v, offs, dev = _ragged_f16(rng, lens, H, KVH, D)
+    a = _run_ragged(engine, dev, lens, H, KVH, D)
+    b = _run_ragged(rows_engine, dev, lens, H, KVH, D)
+    assert np.allclose(a, b, rtol=2e-5, atol=2e-6), np.max(np.abs(a - b))
+    for i in (0, 17, 31):
+        sl = slice(offs[i], offs[i] + lens[i])
+        _close(b[i], O.attention(q[i], k[sl], v[sl], H, KVH, D))

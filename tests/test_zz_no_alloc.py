@@ -68,11 +68,17 @@ def test_noalloc_rejects_partials_above_scratch():
         buf = (C.c_float * 4)()
         lens = (C.c_int32 * 64)()
         p = C.cast(buf, C.c_void_p)
-        # 64 sequences up to 2^20 positions: far more split partials than the scratch holds
-        st = lib.janus_attention_noalloc(h, p, p, p, _lib.DT_F16, p, 64, 32, 8, 128, 0, 1 << 20, None,
+        # 64 sequences up to 2^20 positions with 64-dim heads (the piece plan,
+        # partials per sequence and piece): far more than the scratch holds
+        st = lib.janus_attention_noalloc(h, p, p, p, _lib.DT_F16, p, 64, 32, 8, 64, 0, 1 << 20, None,
                                          C.cast(lens, C.c_void_p), 1 << 20, 0.0)
         assert st == _lib.E_INVALID_DIM
         assert b"fixed scratch" in lib.janus_last_error(h)
+        # the same batch with 128-dim heads streams whole rows, whose partials
+        # are per workgroup (two slots) whatever the lengths: within the scratch
+        st = lib.janus_attention_noalloc(h, p, p, p, _lib.DT_F16, p, 64, 32, 8, 128, 0, 1 << 20, None,
+                                         C.cast(lens, C.c_void_p), 1 << 20, 0.0)
+        assert st == _lib.E_NO_DEVICE
         # a shape within the scratch passes the host checks and then needs a device
         st = lib.janus_attention_noalloc(h, p, p, p, _lib.DT_F16, p, 1, 32, 8, 128, 100, 128, None, None, 0, 0.0)
         assert st == _lib.E_NO_DEVICE
