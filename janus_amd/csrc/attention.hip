@@ -297,6 +297,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnArgs a) {
 }
 
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef _Float16 ah4 __attribute__((ext_vector_type(4)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 
 // Binary16 caches: one wavefront attends G query heads of one KV head over a
@@ -603,8 +604,7 @@ struct RowsLds {
     static constexpr uint32_t NDMA = RBP / KVH * (RB / 1024) * 2;   // 1 KB requests per wavefront per block
     static constexpr uint32_t QW = G * D * 4;         // q of a wavefront's G heads (fp32)
     static constexpr uint32_t NQ = (QW + 1023) / 1024;   // requests for it
-    static constexpr uint32_t PW = RBP * G + G;       // floats of a wavefront's P area
-    static constexpr uint32_t BYTES = 2 * BUF + KVH * QW + KVH * PW * 4;
+    static constexpr uint32_t BYTES = 2 * BUF + KVH * QW;
 };
 
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
@@ -628,16 +628,14 @@ template <uint32_t N> __device__ __forceinline__ void wait_vm() {
 template <int D, int G, int KVH>
 __global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
     using L = RowsLds<D, G, KVH>;
-    constexpr int KS = D / 32, LPP = D / 8, SLOTS = 64 / LPP, STEPS = RBP / SLOTS;
+    constexpr int KS = D / 32, NT = D / 16;
     static_assert(D == 128 && (KVH == 4 || KVH == 8) && L::NDMA == 8 && G <= 8, "row streaming: D 128, 4 or 8 KV heads");
     static_assert(L::BYTES <= 160 * 1024, "row streaming: LDS");
     __shared__ __align__(16) unsigned char lds[L::BYTES];
     const int lane = threadIdx.x & 63;
     const uint32_t kvh = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    unsigned char *qw = lds + 2 * L::BUF + kvh * L::QW;                        // this wavefront's q
-    float *Pw = (float *)(lds + 2 * L::BUF + KVH * L::QW) + kvh * L::PW;      // and P area
-    const int slot = lane / LPP, dl = lane % LPP;   // P.V layout
-    const int col = lane & 15, grp = lane >> 4;     // MFMA layout
+    unsigned char *qw = lds + 2 * L::BUF + kvh * L::QW;   // this wavefront's q
+    const int col = lane & 15, grp = lane >> 4;           // MFMA layout
     const RowsPlan f = rows_plan(a, lane, gridDim.x);
     const uint32_t w = blockIdx.x;
     if (w >= f.nwg) return;
@@ -686,7 +684,9 @@ __global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
 
     ah8 qh[KS], qm[KS], ql[KS];
     float sc2 = 0.0f;
-    float m = -INFINITY, l = 0.0f, acc[G][8];
+    // acc[t]: o^T for dims 16t + 4*grp + e (e = 0..3) of head `col`, scaled by 2^14
+    float m = -INFINITY, l = 0.0f;
+    af4 acc[NT];
 
     Blk cur = locate(i0);
     bool cur_start = true;
@@ -755,9 +755,7 @@ __global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
                     ql[t][e] = (_Float16)(r - (float)mid);
                 }
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+            for (int t = 0; t < NT; ++t) acc[t] = af4{0.0f, 0.0f, 0.0f, 0.0f};
             m = -INFINITY;
             l = 0.0f;
             // q of the next sequence, when its first block is in this range;
@@ -800,73 +798,57 @@ __global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
             for (int r = 0; r < 4; ++r) ps[r] = mn == -INFINITY ? 0.0f : fexp2(sv[r] - mn);
             l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
             m = mn;
-            if (col < G) {
+            // o^T += V^T P^T on v_mfma_f32_16x16x16_f16: A = V^T (dims x the
+            // block's 16 positions, gathered from the LDS rows), B = P^T
+            // straight from the softmax layout (lane = head col, positions
+            // 4*grp + e) as binary16 hi + lo parts of 2^14 p (22 significant
+            // bits; p below 2^-38 of the running maximum flushes to zero).
+            // The rescale is per lane: every lane's column is its own head.
+            ah4 ph, pl;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) Pw[(4 * grp + r) * G + col] = ps[r];
-                if (grp == 0) Pw[RBP * G + col] = alpha;
+            for (int r = 0; r < 4; ++r) {
+                const float x = ps[r] * 16384.0f;
+                const _Float16 hi = (_Float16)x;
+                ph[r] = hi;
+                pl[r] = (_Float16)(x - (float)hi);
             }
-            // the area is read by other lanes of this wavefront only: LDS
-            // operations of one wavefront complete in order
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const unsigned char *vcol = vt + (4 * grp) * L::RP + kvh * D * 2 + col * 2;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float al = Pw[RBP * G + g];
+            for (int t = 0; t < NT; ++t) {
+                ah4 va;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] *= al;
+                for (int e = 0; e < 4; ++e) va[e] = *(const _Float16 *)(vcol + e * L::RP + 32 * t);
+                acc[t] *= alpha;
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc[t], 0, 0, 0);
             }
-#pragma unroll
-            for (int u = 0; u < STEPS; ++u) {
-                const float *pr = Pw + (u * SLOTS + slot) * G;
-                KVRow<_Float16> vrow;
-                vrow.r = *(const uint4 *)(vt + (u * SLOTS + slot) * L::RP + kvh * D * 2 + 16 * dl);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float pg = pr[g];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg, vrow.get(e), acc[g][e]);
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
 
         if (cur_end) {
-            // slots share the running maximum: sum acc over slots, l over the 4 position groups
-            // (in place: the next block starts a segment and clears acc)
+            // l over the 4 position groups; o^T is complete in every lane
             float lt = l + lane_xor<16>(l);
             lt += lane_xor<32>(lt);
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    acc[g][e] += lane_xor<16>(acc[g][e]);
-                    acc[g][e] += lane_xor<32>(acc[g][e]);
-                }
             // the sequence's blocks all lie in this workgroup's range: write
             // the output; else a partial in slot 0 (the segment that holds the
             // range's first block) or slot 1 (the one that runs past its end)
             const bool whole = rows_owner(f, cur.first) == w && rows_owner(f, cur.first + cur.nb - 1) == w;
             const uint32_t slot2 = cur.first <= i0 ? 0u : 1u;
-            const bool writer = lane < LPP;
+            if (col < G) {
+                const uint32_t h = kvh * G + col;
+                if (whole) {
+                    const float inv = (1.0f / 16384.0f) / fmaxf(lt, 1e-20f);
+                    const size_t at0 = ((size_t)cur.b * a.heads + h) * D + 4 * grp;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float mg = __shfl(m, g, 64), lg = __shfl(lt, g, 64);
-                const uint32_t h = kvh * G + g;
-                if (writer) {
-                    if (whole) {
-                        const float inv = 1.0f / fmaxf(lg, 1e-20f);
-                        const size_t at0 = ((size_t)cur.b * a.heads + h) * D + 8 * dl;
+                    for (int t = 0; t < NT; ++t)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) put_out(a, at0 + e, acc[g][e] * inv);
-                    } else {
-                        float *ws = a.ws + (((size_t)w * 2 + slot2) * a.heads + h) * (D + 2);
-                        if (dl == 0) { ws[0] = mg; ws[1] = lg; }
+                        for (int e = 0; e < 4; ++e) put_out(a, at0 + 16 * t + e, acc[t][e] * inv);
+                } else {
+                    float *ws = a.ws + (((size_t)w * 2 + slot2) * a.heads + h) * (D + 2);
+                    if (grp == 0) { ws[0] = m; ws[1] = lt; }
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) ws[2 + 8 * dl + e] = acc[g][e];
-                    }
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ws[2 + 16 * t + 4 * grp + e] = acc[t][e] * (1.0f / 16384.0f);
                 }
             }
         }
