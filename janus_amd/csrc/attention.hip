@@ -869,11 +869,14 @@ __global__ __launch_bounds__(64 * KVH) void attn_rows_kernel(AttnArgs a) {
 // Merge of the row-streaming split: sequence b's segments are the partials
 // of the workgroups whose ranges meet its blocks ([w][slot][head][D + 2]:
 // slot 0 when the sequence holds the range's first block, else slot 1); a
-// sequence inside one range was written directly. Lane j of each 64-segment
-// chunk reads segment j's (m, l) and weight, so the maxima and sums take one
-// round trip per chunk, and the o loads of a chunk are all independent.
+// sequence inside one range was written directly. Per chunk of 32 segments,
+// lane j finds segment j's partial; the o loads of every segment of the
+// chunk are issued with the (m, l) loads (their addresses do not depend on
+// the loaded values), so a chunk costs one memory round trip after the
+// length table.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_rows_kernel(AttnArgs a, uint32_t nwg_grid) {
+    constexpr int CH = 32;
     const uint32_t h = blockIdx.x, b = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const RowsPlan f = rows_plan(a, lane, nwg_grid);
@@ -881,57 +884,52 @@ __global__ __launch_bounds__(D) void attn_merge_rows_kernel(AttnArgs a, uint32_t
     const uint32_t first = (uint32_t)__shfl((int)(f.incl - f.nbk), (int)b, 64);
     const uint32_t w0 = rows_owner(f, first), ns = rows_owner(f, first + nb - 1) - w0 + 1;
     if (ns <= 1) return;
-    __shared__ float e_s[D / 64][64];
-    __shared__ uint32_t off_s[D / 64][64];
+    __shared__ uint32_t off_s[D / 64][CH];
+    __shared__ float e_s[D / 64][CH];
     const int wv = threadIdx.x >> 6;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (uint32_t j0 = 0; j0 < ns; j0 += 64) {
-        const uint32_t j = j0 + lane, cnt = min(ns - j0, 64u);
-        float mj = -INFINITY, lj = 0.0f;
-        uint32_t offj = 0;
-        if (j < ns) {
+    for (uint32_t j0 = 0; j0 < ns; j0 += CH) {
+        const uint32_t j = j0 + lane;
+        const bool mine = lane < CH && j < ns;
+        uint32_t offj = 0;   // idle lanes point at a valid partial; their weight is zero
+        if (mine) {
             const uint32_t wj = w0 + j;
             const uint32_t slot = first <= rows_begin(f, wj) ? 0u : 1u;
-            offj = (((uint32_t)wj * 2 + slot) * a.heads + h) * (D + 2);
-            mj = a.ws[offj];
-            lj = a.ws[offj + 1];
+            offj = ((wj * 2 + slot) * a.heads + h) * (D + 2);
         }
-        float Mc = mj;
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, s, 64));
-        const float Mn = fmaxf(M, Mc);
-        if (Mn == -INFINITY) continue;   // no live segment yet
-        const float r = fexp2(M - Mn);   // 0 while M = -inf
-        const float ej = fexp2(mj - Mn); // 0 for dead segments and idle lanes
-        float ls = lj * ej;
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) ls += __shfl_xor(ls, s, 64);
-        L = L * r + ls;
-        o *= r;
-        // weights and offsets through this wavefront's LDS slots, so the o
-        // loads of 16 segments go out together
-        e_s[wv][lane] = ej;
-        off_s[wv][lane] = offj;
+        if (lane < CH) off_s[wv][lane] = offj;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (uint32_t jj = 0; jj < cnt; jj += 16) {
-            float ov[16], ev[16];
+        float ov[CH];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const bool in = jj + k < cnt;
-                const uint32_t q = in ? jj + k : jj;
-                ev[k] = in ? e_s[wv][q] : 0.0f;
-                ov[k] = a.ws[off_s[wv][q] + 2 + threadIdx.x];
-            }
+        for (int k = 0; k < CH; ++k) ov[k] = a.ws[off_s[wv][k] + 2 + threadIdx.x];
+        const float mj = mine ? a.ws[offj] : -INFINITY;
+        const float lj = mine ? a.ws[offj + 1] : 0.0f;
+        float Mc = mj;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) o = fmaf(ev[k], ov[k], o);
+        for (int s2 = 32; s2 >= 1; s2 >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, s2, 64));
+        const float Mn = fmaxf(M, Mc);
+        if (Mn != -INFINITY) {           // else no live segment yet
+            const float r = fexp2(M - Mn);   // 0 while M = -inf
+            const float ej = fexp2(mj - Mn); // 0 for dead segments and idle lanes
+            float ls = lj * ej;
+#pragma unroll
+            for (int s2 = 32; s2 >= 1; s2 >>= 1) ls += __shfl_xor(ls, s2, 64);
+            L = L * r + ls;
+            o *= r;
+            if (lane < CH) e_s[wv][lane] = ej;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int k = 0; k < CH; ++k) o = fmaf(e_s[wv][k], ov[k], o);
+            M = Mn;
         }
         // the slots are rewritten by the next chunk
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        M = Mn;
     }
     put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
 }
