@@ -981,7 +981,9 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
     if (a.qh_div) {   // one query head per workgroup
         dim3 grid(a.splits, a.heads, a.batch), block(64 * a.nw);
         const size_t lds = (size_t)a.nw * (D + 2) * 4;
-        hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 16>), grid, block, lds, ctx->stream, a);
+        if (a.nw == 4) hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 4>), grid, block, lds, ctx->stream, a);
+        else if (a.nw == 8) hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 8>), grid, block, lds, ctx->stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 16>), grid, block, lds, ctx->stream, a);
         JANUS_LAUNCH_CHECK(ctx);
         if (a.splits > 1) {
             hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
@@ -1106,7 +1108,10 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
     uint64_t chunk = (max_len * groups + waves - 1) / waves;
     chunk = (chunk + TP - 1) / TP * TP;
-    const uint32_t nw = qh ? 16 : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
+    // per-query-head launches: 4 wavefronts up to 512 positions (bs=1 decode
+    // step 1.520 against 1.528 ms/token with 16 at contexts 148-348), 16 beyond
+    const uint32_t qh_nw = ctx->attn_qh_nw ? ctx->attn_qh_nw : (max_len <= 512 ? 4u : 16u);
+    const uint32_t nw = qh ? qh_nw : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
     if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
     *chunk_out = (uint32_t)chunk;
     *nw_out = nw;

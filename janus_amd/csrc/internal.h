@@ -42,6 +42,9 @@ struct janus_ctx {
     // whole cache rows through LDS, one workgroup per CU (JANUS_ATTN_ROWS:
     // 0 never, 1 whenever the shape allows, unset: planned)
     int attn_rows = -1;
+    // wavefronts per workgroup of the per-query-head attention launch (short
+    // contexts, few sequences): 4, 8 or 16 (JANUS_ATTN_QH_NW; 0: planned)
+    uint32_t attn_qh_nw = 0;
     // small-M quantised GEMMs over several K passes per workgroup use the
     // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
     bool gemm_pipe = true;

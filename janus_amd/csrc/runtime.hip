@@ -337,6 +337,10 @@ int janus_create(int hip_device, janus_ctx **out) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 1 && v <= 64) ctx->gemm_ks = (uint32_t)v;
     }
+    if (const char *k = std::getenv("JANUS_ATTN_QH_NW")) {
+        const long v = std::strtol(k, nullptr, 10);
+        if (v == 4 || v == 8 || v == 16) ctx->attn_qh_nw = (uint32_t)v;
+    }
     if (const char *k = std::getenv("JANUS_ATTN_ROWS")) {
         if (!std::strcmp(k, "0")) ctx->attn_rows = 0;
         else if (!std::strcmp(k, "1")) ctx->attn_rows = 1;
