@@ -550,12 +550,14 @@ __global__ __launch_bounds__(256) void attn_task_kernel(AttnArgs a) {
 // whole contiguous rows: per 16-position block its wavefronts copy 16 K rows
 // and 16 V rows straight into LDS (LDS-DMA loads, 1 KB each, rows padded by 16
 // bytes so the MFMA operand reads hit every bank), double buffered across
-// blocks and sequences, and each wavefront runs the block step of MfmaAttn
-// for its KV head from LDS (scores on MFMA, online softmax, P.V on the VALU).
-// Work split: the blocks of all sequences, in order, are divided into equal
-// contiguous ranges, one per active workgroup (at least a.chunk blocks each);
-// a sequence spread over several ranges writes one (m, l, o) partial per
-// range for attn_merge_rows_kernel. Lengths are clamped to max_len. batch <= 64.
+// blocks and sequences, and each wavefront runs the block step for its KV
+// head from LDS: scores on MFMA as in MfmaAttn, online softmax, and P.V on
+// MFMA as o^T += V^T P^T. Work split: the blocks of all sequences, in order,
+// are divided into equal contiguous ranges, one per active workgroup (at least
+// a.chunk blocks each); a sequence spread over several ranges writes one
+// (m, l, o) partial per range, in the range's two slots (the segment holding
+// its first block, the one running past its end), for attn_merge_rows_kernel.
+// Lengths are clamped to max_len. batch <= 64.
 constexpr int RBP = 16;   // positions per block
 
 struct RowsPlan {
