@@ -1094,39 +1094,33 @@ __device__ __forceinline__ void store_x16(const float (&v)[16], uint32_t g, _Flo
 }
 
 // RMS-normalised staging of f32 x (workgroups of 512 or 1024 threads,
-// k <= 16 * 512 * MAXG): every thread loads its 16-element groups once, with all loads in flight
-// together; the sum of squares is reduced over the workgroup in a fixed order
-// (thread order, then wavefront order), then x * (1 / rms) * gamma is staged.
+// k <= 16 * 512 * MAXG). Thread t holds the float4 slots s = t + nt * j
+// (elements 4s..4s+3), so each load instruction of a wavefront reads 1 KiB of
+// consecutive bytes, and a 16-element group of the staging is one lane quad.
+// All loads are in flight together; the sum of squares is reduced in a fixed
+// order (the thread's slots, the wavefront by permlane / DPP steps, then
+// wavefront order), then x * (1 / rms) * gamma is staged.
 // The loads (norm_load) are requested before the weights: loads return in
 // issue order, so x requested after the weights would hold the reduction and
 // its barriers until every weight load had landed.
-template <int MAXG> struct NormRegs { float v[MAXG][16], gm[MAXG][16]; };
+template <int MAXG> struct NormRegs { jf4 v[4 * MAXG], gm[4 * MAXG]; };
 
 template <int MAXG>
 __device__ __forceinline__ void norm_load(const float *__restrict__ x, const float *__restrict__ gamma, uint32_t k,
                                           uint32_t nt, NormRegs<MAXG> &r) {
-    auto &v = r.v;
-    auto &gm = r.gm;
     // x and gamma are requested together: one round trip before the reduction
 #pragma unroll
-    for (int j = 0; j < MAXG; ++j) {
-        const uint32_t g = threadIdx.x + nt * j, e0 = g * 16;
-        if (e0 + 16 <= k) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const jf4 xa = *(const jf4 *)(x + e0 + 4 * q), ga = *(const jf4 *)(gamma + e0 + 4 * q);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    v[j][4 * q + t] = xa[t];
-                    gm[j][4 * q + t] = ga[t];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                v[j][t] = e0 + t < k ? x[e0 + t] : 0.0f;
-                gm[j][t] = e0 + t < k ? gamma[e0 + t] : 0.0f;
-            }
+    for (int j = 0; j < 4 * MAXG; ++j) {
+        // Rounds with no slot of the staging load nothing (a workgroup-uniform
+        // branch; their registers are never read). k % 8 == 0 for every weight
+        // format these kernels take, so a slot is whole or past the end; slots
+        // past the end load the last slot again and are zeroed in the staging
+        // (a per-lane conditional load makes the compiler merge registers and
+        // wait for the load before the weights are requested).
+        if (nt * j < 4 * ((k + 15) / 16)) {
+            const uint32_t sl = min(threadIdx.x + nt * j, k / 4 - 1);
+            r.v[j] = *(const jf4 *)(x + 4 * sl);
+            r.gm[j] = *(const jf4 *)(gamma + 4 * sl);
         }
     }
 }
@@ -1134,15 +1128,18 @@ __device__ __forceinline__ void norm_load(const float *__restrict__ x, const flo
 template <bool PERM, int MAXG>
 __device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, uint32_t nt, _Float16 *xs, float *sx16, float eps,
                                float *red) {
-    const uint32_t g16 = (k + 15) / 16;
-    auto &v = r.v;
-    const auto &gm = r.gm;
+    const uint32_t nslot = 4 * ((k + 15) / 16);   // whole 16-element groups (zeros past k)
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MAXG; ++j)
+    for (int j = 0; j < 4 * MAXG; ++j) {
+        if (nt * j >= nslot) break;   // uniform: the round loaded nothing
+        if (4 * (threadIdx.x + nt * j) >= k) r.v[j] = (jf4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int t = 0; t < 16; ++t) ss = fmaf(v[j][t], v[j][t], ss);
-    ss = wave_sum(ss);
+        for (int t = 0; t < 4; ++t) ss = fmaf(r.v[j][t], r.v[j][t], ss);
+    }
+    float sv[1] = {ss};
+    int ridx;
+    ss = reduce_wave_rows<1>(sv, threadIdx.x & 63, ridx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
@@ -1151,12 +1148,21 @@ __device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, uint32_t nt, _Floa
     // is rounded to binary16 right after
     const float inv = 1.0f / sqrtf(tot / (float)k + eps);
 #pragma unroll
-    for (int j = 0; j < MAXG; ++j) {
-        const uint32_t g = threadIdx.x + nt * j;
-        if (g >= g16) continue;
+    for (int j = 0; j < 4 * MAXG; ++j) {
+        if (nt * j >= nslot) break;   // uniform: no slot of this round is staged
+        const uint32_t sl = threadIdx.x + nt * j, e0 = 4 * sl;
+        _Float16 hv[4];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v[j][t] = (v[j][t] * inv) * gm[j][t];
-        store_x16<PERM>(v[j], g, xs, sx16);
+        for (int t = 0; t < 4; ++t) hv[t] = (_Float16)((r.v[j][t] * inv) * r.gm[j][t]);
+        // the group's sum of its binary16 values: lane, then lane pairs of the quad
+        float q = (((float)hv[0] + (float)hv[1]) + (float)hv[2]) + (float)hv[3];
+        q += dpp_f<0xb1>(q);   // quad_perm [1,0,3,2]
+        q += dpp_f<0x4e>(q);   // quad_perm [2,3,0,1]
+        if (sl < nslot) {
+            if ((threadIdx.x & 3) == 0) sx16[sl >> 2] = q;
+            const jh4 o = PERM ? (jh4){hv[0], hv[2], hv[1], hv[3]} : (jh4){hv[0], hv[1], hv[2], hv[3]};
+            *(jh4 *)(xs + (e0 / 32) * XLayout<_Float16>::STRIDE + (e0 % 32)) = o;
+        }
     }
 }
 
