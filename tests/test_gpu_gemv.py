@@ -83,15 +83,20 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
 @pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704), (1003, 4096), (8200, 4096)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
-    """Every binary16 product of 64+ units per row runs the LDS-staged kernel.
-    (1003, 8704): five units per lane, single-buffered (Q4_0 / Q8_0 with x
-    requested first, K-quants re-reading x from LDS; F16 rows of 1088 units take
-    the register kernel), a last 512-thread workgroup with five idle wavefronts
-    that stream a real row group and discard it. (1003, 4096): F16 with eight
-    units per lane on the double-buffered body, five idle wavefronts; the
-    quantised formats two units per lane, two idle wavefronts. (8200, 4096):
-    4100 row groups of two, enough for 1024-thread workgroups (Q4_0), whose
-    persistent grid gives some wavefronts a second group."""
+    """Every binary16 product of 64+ units per row runs the LDS-staged kernel
+    (512-thread workgroups). (1003, 8704): five units per lane,
+    single-buffered (Q4_0 / Q8_0 with x requested first, K-quants re-reading x
+    from LDS; F16 rows of 1088 units take the register kernel), a last
+    workgroup with five idle wavefronts that stream a real row group and
+    discard it. (1003, 4096): F16 with eight units per lane on the
+    double-buffered body, five idle wavefronts; the quantised formats two
+    units per lane, one row per step, five idle wavefronts. (8200, 4096): 8200
+    row groups of one row (quantised formats), whose persistent grid gives
+    wavefronts a second and third group."""
+    _check_gemv_f16(engine, ggml_type, n, k)
+
+
+def _check_gemv_f16(engine, ggml_type, n, k):
     raw, w = _weight(engine, ggml_type, n, k, 3 * n + k, FTZ[ggml_type])
     rng = np.random.default_rng(n)
     xh = rng.standard_normal(k).astype(np.float16)
@@ -103,6 +108,35 @@ def test_gemv_f16_activations(engine, ggml_type, n, k):
     y64 = O.gemv_f64(wf, x)
     # fp32 accumulation then one binary16 rounding of the output
     assert np.all(np.abs(got - y64) <= _bound(wf, x) + np.abs(y64) * 2.0 ** -11 + 2.0 ** -24)
+
+
+@pytest.fixture(scope="module")
+def wide_engine():
+    """A context whose LDS-staged GEMV takes 1024-thread workgroups wherever
+    the body fits (JANUS_GEMV_LDS_THREADS=1024 is read when the context is
+    made)."""
+    import os
+    from janus_amd.ops import ComputeEngine
+    old = os.environ.get("JANUS_GEMV_LDS_THREADS")
+    os.environ["JANUS_GEMV_LDS_THREADS"] = "1024"
+    try:
+        eng = ComputeEngine(0)
+    finally:
+        if old is None:
+            del os.environ["JANUS_GEMV_LDS_THREADS"]
+        else:
+            os.environ["JANUS_GEMV_LDS_THREADS"] = old
+    yield eng
+    eng.sync()
+    eng.close()
+
+
+@pytest.mark.parametrize("ggml_type", [2, 1])
+@pytest.mark.parametrize("n,k", [(1003, 4096), (8200, 4096)])
+def test_gemv_f16_activations_1024_thread_workgroups(wide_engine, ggml_type, n, k):
+    """The 1024-thread LDS-staged body (Q4_0 and F16 rows of two units per
+    lane): a last workgroup with idle wavefronts, and a persistent grid."""
+    _check_gemv_f16(wide_engine, ggml_type, n, k if ggml_type == 2 else k // 4)
 
 
 def test_gemv_f16_odd_k_generic_path(engine):
