@@ -1443,11 +1443,12 @@ template <class F, int BPL, int R>
 int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     constexpr int TMAX = lds_max_threads<F, BPL>();
     const uint32_t groups = (a.n + R - 1) / R;
-    // 512-thread workgroups, two or more per CU: measured faster than one
-    // 1024-thread workgroup per CU with x staged once per CU (bs=1 decode
-    // 1.564 -> 1.508 ms/token, Q4_0 14336x4096 7.9 -> 7.5-7.8 us);
-    // JANUS_GEMV_LDS_THREADS=1024 selects those where the body fits
-    int threads = 512;
+    // At most one row group per wavefront (16 per CU): 1024-thread
+    // workgroups, x staged once per CU (Q4_0 4096x4096 4.0 -> 3.7 us, the
+    // fused QKV 6.8 -> 6.6). More groups: 512-thread workgroups, two per CU,
+    // whose stagings and barriers do not hold each other's wavefronts (Q4_0
+    // 14336x4096 7.8 -> 7.35 us, gate/up 28672x4096 14.6 -> 13.2).
+    int threads = TMAX == 1024 && groups <= 16u * ctx->num_cus ? 1024 : 512;
     if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) threads = (int)ctx->gemv_lds_threads;
     const int wg_waves = threads / 64;
     // resident workgroups per CU for this kernel at this LDS size (4 KB steps)

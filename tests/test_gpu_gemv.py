@@ -83,16 +83,17 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
 @pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704), (1003, 4096), (8200, 4096)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
-    """Every binary16 product of 64+ units per row runs the LDS-staged kernel
-    (512-thread workgroups). (1003, 8704): five units per lane,
+    """Every binary16 product of 64+ units per row runs the LDS-staged kernel.
+    (1003, 8704): five units per lane,
     single-buffered (Q4_0 / Q8_0 with x requested first, K-quants re-reading x
     from LDS; F16 rows of 1088 units take the register kernel), a last
     workgroup with five idle wavefronts that stream a real row group and
     discard it. (1003, 4096): F16 with eight units per lane on the
     double-buffered body, five idle wavefronts; the quantised formats two
-    units per lane, one row per step, five idle wavefronts. (8200, 4096): 8200
-    row groups of one row (quantised formats), whose persistent grid gives
-    wavefronts a second and third group."""
+    units per lane, one row per step (Q4_0 in 1024-thread workgroups, the
+    rest in 512), idle wavefronts in the last workgroup. (8200, 4096): 8200
+    row groups of one row (quantised formats, 512-thread workgroups), whose
+    persistent grid gives wavefronts a second and third group."""
     _check_gemv_f16(engine, ggml_type, n, k)
 
 
@@ -134,8 +135,9 @@ def wide_engine():
 @pytest.mark.parametrize("ggml_type", [2, 1])
 @pytest.mark.parametrize("n,k", [(1003, 4096), (8200, 4096)])
 def test_gemv_f16_activations_1024_thread_workgroups(wide_engine, ggml_type, n, k):
-    """The 1024-thread LDS-staged body (Q4_0 and F16 rows of two units per
-    lane): a last workgroup with idle wavefronts, and a persistent grid."""
+    """1024-thread workgroups for every LDS-staged body that fits them (Q4_0
+    and F16 rows of two units per lane), also where the default takes 512:
+    a last workgroup with idle wavefronts, and a persistent grid."""
     _check_gemv_f16(wide_engine, ggml_type, n, k if ggml_type == 2 else k // 4)
 
 
