@@ -1443,22 +1443,27 @@ template <class F, int BPL, int R>
 int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     constexpr int TMAX = lds_max_threads<F, BPL>();
     const uint32_t groups = (a.n + R - 1) / R;
-    // At most one row group per wavefront (16 per CU): 1024-thread
-    // workgroups, x staged once per CU (Q4_0 4096x4096 4.0 -> 3.7 us, the
-    // fused QKV 6.8 -> 6.6). More groups: 512-thread workgroups, two per CU,
-    // whose stagings and barriers do not hold each other's wavefronts (Q4_0
+    // At most one row group per wavefront (16 per CU): one workgroup per CU
+    // with a wavefront per group, x staged once per CU (Q4_0 4096x4096 in
+    // 1024 threads 4.0 -> 3.7 us; the fused QKV's 3072 groups in 768 threads
+    // 6.8 -> 6.4). More groups: 512-thread workgroups, two per CU, whose
+    // stagings and barriers do not hold each other's wavefronts (Q4_0
     // 14336x4096 7.8 -> 7.35 us, gate/up 28672x4096 14.6 -> 13.2).
-    int threads = TMAX == 1024 && groups <= 16u * ctx->num_cus ? 1024 : 512;
+    int threads = 512;
+    if (TMAX == 1024 && groups <= 16u * ctx->num_cus) {
+        const uint32_t w = (groups + ctx->num_cus - 1) / ctx->num_cus;   // wavefronts for one workgroup per CU
+        threads = w <= 8 ? 512 : (int)(64 * w);
+    }
     if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) threads = (int)ctx->gemv_lds_threads;
     const int wg_waves = threads / 64;
     // resident workgroups per CU for this kernel at this LDS size (4 KB steps)
-    static int per_cu[2][2][17] = {};
+    static int per_cu[2][5][17] = {};
     const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
     const uint32_t nblk = (a.k + XB - 1) / XB;
     const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
     const size_t lds_step = (lds + 4095) / 4096;
-    int &occ = per_cu[norm ? 1 : 0][threads == 1024][lds_step];
+    int &occ = per_cu[norm ? 1 : 0][threads / 256][lds_step];
     if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_step * 4096) != hipSuccess || nb < 1)
