@@ -1093,7 +1093,7 @@ __device__ __forceinline__ void store_x16(const float (&v)[16], uint32_t g, _Flo
     }
 }
 
-// RMS-normalised staging of f32 x (workgroups of 512 or 1024 threads,
+// RMS-normalised staging of f32 x (workgroups of 512 to 1024 threads,
 // k <= 16 * 512 * MAXG). Thread t holds the float4 slots s = t + nt * j
 // (elements 4s..4s+3), so each load instruction of a wavefront reads 1 KiB of
 // consecutive bytes, and a 16-element group of the staging is one lane quad.
@@ -1457,13 +1457,13 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) threads = (int)ctx->gemv_lds_threads;
     const int wg_waves = threads / 64;
     // resident workgroups per CU for this kernel at this LDS size (4 KB steps)
-    static int per_cu[2][5][17] = {};
+    static int per_cu[2][17][17] = {};
     const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
     const uint32_t nblk = (a.k + XB - 1) / XB;
     const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
     const size_t lds_step = (lds + 4095) / 4096;
-    int &occ = per_cu[norm ? 1 : 0][threads / 256][lds_step];
+    int &occ = per_cu[norm ? 1 : 0][wg_waves][lds_step];
     if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_step * 4096) != hipSuccess || nb < 1)
