@@ -1110,9 +1110,10 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
     uint64_t chunk = (max_len * groups + waves - 1) / waves;
     chunk = (chunk + TP - 1) / TP * TP;
-    // per-query-head launches: 4 wavefronts up to 512 positions (bs=1 decode
-    // step 1.520 against 1.528 ms/token with 16 at contexts 148-348), 16 beyond
-    const uint32_t qh_nw = ctx->attn_qh_nw ? ctx->attn_qh_nw : (max_len <= 512 ? 4u : 16u);
+    // per-query-head launches: 8 wavefronts up to 512 positions (bs=1 decode
+    // step at contexts 148-348: 1.458 ms/token against 1.480 with 4 and with
+    // 16), 16 beyond
+    const uint32_t qh_nw = ctx->attn_qh_nw ? ctx->attn_qh_nw : (max_len <= 512 ? 8u : 16u);
     const uint32_t nw = qh ? qh_nw : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
     if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
     *chunk_out = (uint32_t)chunk;
