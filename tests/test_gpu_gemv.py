@@ -81,7 +81,8 @@ def test_gemv_f32_matches_oracle(engine, ggml_type, n, k):
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
-@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704), (1003, 4096), (8200, 4096)])
+@pytest.mark.parametrize("n,k", [(33, 256), (512, 4096), (64, 11008), (1003, 8704), (1003, 4096), (8200, 4096),
+                                 (2500, 4096)])
 def test_gemv_f16_activations(engine, ggml_type, n, k):
     """Every binary16 product of 64+ units per row runs the LDS-staged kernel.
     (1003, 8704): five units per lane,
@@ -93,7 +94,9 @@ def test_gemv_f16_activations(engine, ggml_type, n, k):
     units per lane, one row per step (Q4_0 in 1024-thread workgroups, the
     rest in 512), idle wavefronts in the last workgroup. (8200, 4096): 8200
     row groups of one row (quantised formats, 512-thread workgroups), whose
-    persistent grid gives wavefronts a second and third group."""
+    persistent grid gives wavefronts a second and third group. (2500, 4096):
+    Q4_0 with ten groups per CU on a 256-CU device, one 640-thread
+    workgroup per CU."""
     _check_gemv_f16(engine, ggml_type, n, k)
 
 
@@ -139,6 +142,14 @@ def test_gemv_f16_activations_1024_thread_workgroups(wide_engine, ggml_type, n, 
     and F16 rows of two units per lane), also where the default takes 512:
     a last workgroup with idle wavefronts, and a persistent grid."""
     _check_gemv_f16(wide_engine, ggml_type, n, k if ggml_type == 2 else k // 4)
+
+
+@pytest.mark.parametrize("n", [2500, 3000])
+def test_gemv_f16_rows_one_workgroup_per_cu(engine, n):
+    """F16 rows of two units per lane (k = 1024), one row per step: 2500 and
+    3000 groups give one workgroup per CU of 640 and 768 threads on a 256-CU
+    device."""
+    _check_gemv_f16(engine, 1, n, 1024)
 
 
 def test_gemv_f16_odd_k_generic_path(engine):
