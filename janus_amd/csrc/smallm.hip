@@ -1118,7 +1118,7 @@ __global__ __launch_bounds__(1024) void epi_resnorm_kernel(GemmPartials p, const
         s = fmaf(v[j].z, v[j].z, s);
         s = fmaf(v[j].w, v[j].w, s);
     }
-    s = wave_sum(s);
+    s = wave_sum_dpp(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     float tot = 0.0f;
