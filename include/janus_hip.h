@@ -43,7 +43,9 @@ typedef enum janus_status {
     JANUS_E_TOKEN_RANGE = 5,       /* token id >= vocab (model/transformer/embedding.rs:33-39) */
     JANUS_E_HIP = 6,               /* ComputeError::KernelExecutionFailed */
     JANUS_E_OOM = 7,               /* ComputeError::BufferCreationFailed */
-    JANUS_E_NO_DEVICE = 8          /* no adapter (compute/engine.rs:32-39) */
+    JANUS_E_NO_DEVICE = 8,         /* no adapter (compute/engine.rs:32-39) */
+    JANUS_E_NAN_LOGITS = 9         /* NaN logits under the CPU-path greedy rules; the reference
+                                      panics (model/sampler.rs:191-193, 397-399) */
 } janus_status;
 
 /* Tensor element types use GGML's type ids (formats/gguf/types.rs:80-187). */

@@ -82,7 +82,10 @@ int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq);
  * is not returned, as the reference does not push it). Runs on the device:
  * the decode step is captured once and replayed, the penalty's context is
  * kept as occurrence counts on the device and the sampled tokens are read
- * back in chunks. Sets the model's sampler (janus_model_set_sampler). */
+ * back in chunks. Sets the model's sampler (janus_model_set_sampler).
+ * Under the penalty rule a NaN among a step's logits ends the call with
+ * JANUS_E_NAN_LOGITS, where the reference's CPU sampler panics
+ * (sampler.rs:191-193); the GPU-argmax rule ignores NaN as argmax.wgsl does. */
 int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
                          float repetition_penalty, uint32_t *out_tokens, uint32_t *n_out);
 /* Model::generate_batch (generation.rs:673-870) with continuous batching:
@@ -96,7 +99,8 @@ int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prom
  * Sampler::sample_batch (sampler.rs:379-428): the penalty over that
  * request's generated tokens, then the last-max argmax. Output: request i's
  * tokens at out_tokens[i * max_tokens], n_out[i] of them. Sets the model's
- * sampler. */
+ * sampler. A NaN among any row's logits ends the call with
+ * JANUS_E_NAN_LOGITS (sample_batch panics, sampler.rs:397-399). */
 int janus_model_generate_batch(janus_model *m, const uint32_t *prompts, const uint32_t *prompt_lens, uint32_t nreq,
                                uint32_t max_tokens, float repetition_penalty, uint32_t *out_tokens, uint32_t *n_out);
 
@@ -117,6 +121,10 @@ int janus_model_set_sampler(janus_model *m, int mode, float repetition_penalty);
 int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq);
 int janus_model_graph_begin_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
                                   const uint32_t *slots, uint32_t nseq);
+/* graph_run returns once the steps have run (it synchronises the context's
+ * stream). Under JANUS_SAMPLER_ARGMAX or _PENALTY a NaN among a sequence's
+ * logits stops that sequence (its generated tokens end before that step) and
+ * the call returns JANUS_E_NAN_LOGITS (sampler.rs:191-193, 397-399). */
 int janus_model_graph_run(janus_model *m, uint32_t steps);
 /* The token each sequence consumes next (the last one chosen). */
 int janus_model_graph_read_tokens(janus_model *m, uint32_t *h_tokens, uint32_t nseq);

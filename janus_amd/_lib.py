@@ -24,6 +24,7 @@ E_TOKEN_RANGE = 5
 E_HIP = 6
 E_OOM = 7
 E_NO_DEVICE = 8
+E_NAN_LOGITS = 9
 
 # GGML type ids (janus_dtype)
 DT_F32 = 0

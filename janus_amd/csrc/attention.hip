@@ -612,13 +612,17 @@ struct RowsLds {
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
 // (non-temporal; lds is wavefront-uniform and goes to M0). Issued as inline
 // assembly so that the compiler tracks none of these requests: every wait for
-// them is an explicit vmcnt wait below. M0 is not named as clobbered (the
-// compiler reserves it); the kernels that call this make no other use of M0.
+// them is an explicit vmcnt wait below. M0 is named as clobbered, so the
+// statement defines M0 for the compiler and no value of its own is assumed to
+// survive it (clang warns that M0 is a reserved register; that is the point).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src),
                  "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
+                 : "memory", "m0");
 }
+#pragma clang diagnostic pop
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
@@ -890,10 +894,14 @@ __global__ __launch_bounds__(D) void attn_merge_rows_kernel(AttnArgs a, uint32_t
     __shared__ float e_s[D / 64][CH];
     const int wv = threadIdx.x >> 6;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
+    // Idle lanes read the sequence's first segment (workgroup w0 always writes
+    // it, since ns >= 2), so the zero weight they apply multiplies a partial of
+    // this launch, never stale workspace bits (0 * inf would be NaN).
+    const uint32_t off0 = ((w0 * 2 + (first <= rows_begin(f, w0) ? 0u : 1u)) * a.heads + h) * (D + 2);
     for (uint32_t j0 = 0; j0 < ns; j0 += CH) {
         const uint32_t j = j0 + lane;
         const bool mine = lane < CH && j < ns;
-        uint32_t offj = 0;   // idle lanes point at a valid partial; their weight is zero
+        uint32_t offj = off0;
         if (mine) {
             const uint32_t wj = w0 + j;
             const uint32_t slot = first <= rows_begin(f, wj) ? 0u : 1u;

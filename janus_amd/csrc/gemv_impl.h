@@ -27,6 +27,7 @@
 //    butterfly (log2 R exchange steps that halve the live values, then a
 //    plain xor butterfly), so the reduction costs O(R + log LPR) shuffles.
 #pragma once
+#include <atomic>
 #include <type_traits>
 
 #include "internal.h"
@@ -1359,12 +1360,13 @@ int launch_one(janus_ctx *ctx, const GemvArgs &a) {
     const uint32_t nblk = (a.k + XB - 1) / XB;
     size_t lds = ((nblk * XLayout<XT>::STRIDE * sizeof(XT) + 15) & ~(size_t)15) + ((a.k + 15) / 16) * 4;
     if (lds > 160 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
-    static bool attr_set = false;   // allow > 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU)
-    if (!attr_set) {
+    // allow > 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU); thread-safe one-time set-up
+    static const bool attr_set = [] {
         (void)hipFuncSetAttribute((const void *)gemv_kernel<F, XIN, XT, LPR, R, BPL>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
-    }
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        return true;
+    }();
+    (void)attr_set;
     hipLaunchKernelGGL((gemv_kernel<F, XIN, XT, LPR, R, BPL>), dim3(grid), dim3(threads), lds, ctx->stream, a);
     JANUS_LAUNCH_CHECK(ctx);
     return JANUS_OK;
@@ -1391,13 +1393,17 @@ int launch_fmt(janus_ctx *ctx, const GemvArgs &a) {
 // per CU); each wavefront then walks several row groups.
 template <class F, typename XT, int BPL, int R>
 int launch_reg(janus_ctx *ctx, const GemvArgs &a) {
-    static int occ = 0;
+    // host threads may launch at once: the cached value is relaxed-atomic (a
+    // race only repeats the same occupancy query)
+    static std::atomic<int> occ_cache{0};
+    int occ = occ_cache.load(std::memory_order_relaxed);
     if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_reg_kernel<F, XT, BPL, R>, 256, 0) != hipSuccess ||
             nb < 1)
             nb = 1;
         occ = nb;
+        occ_cache.store(occ, std::memory_order_relaxed);
     }
     int per_cu = occ < (int)ctx->gemv_wpc / 4 ? occ : (int)ctx->gemv_wpc / 4;
     if (per_cu < 1) per_cu = 1;
@@ -1457,18 +1463,20 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) threads = (int)ctx->gemv_lds_threads;
     const int wg_waves = threads / 64;
     // resident workgroups per CU for this kernel at this LDS size (4 KB steps)
-    static int per_cu[2][17][17] = {};
+    static std::atomic<int> per_cu[2][17][17] = {};   // relaxed, as in launch_reg
     const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
     const uint32_t nblk = (a.k + XB - 1) / XB;
     const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
     const size_t lds_step = (lds + 4095) / 4096;
-    int &occ = per_cu[norm ? 1 : 0][wg_waves][lds_step];
+    std::atomic<int> &occ_cache = per_cu[norm ? 1 : 0][wg_waves][lds_step];
+    int occ = occ_cache.load(std::memory_order_relaxed);
     if (occ == 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_step * 4096) != hipSuccess || nb < 1)
             nb = 1;
         occ = nb;
+        occ_cache.store(occ, std::memory_order_relaxed);
     }
     const int wg_cap = (int)ctx->gemv_lds_wpc / wg_waves;
     int pc = occ < wg_cap ? occ : wg_cap;

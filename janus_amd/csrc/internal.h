@@ -304,7 +304,14 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     return ((uint64_t)k << 32) | idx;
 }
 
+// Key of a NaN logit under SAMPLE_ARGMAX and SAMPLE_PENALTY: above every
+// other key, so a row's running maximum carries it to the step's consumer,
+// which refuses the step (the reference's CPU sampler panics on NaN logits,
+// sampler.rs:191-193 and 397-399). SAMPLE_WGSL never produces it.
+constexpr uint64_t kNanKey = ~0ull;
+
 // Argmax key of logit v at index idx under the sampler state s.
+//  SAMPLE_ARGMAX / SAMPLE_PENALTY: a NaN v gives kNanKey.
 //  SAMPLE_PENALTY: v first takes the repetition penalty once per occurrence
 //    of idx among the generated tokens (count; sampler.rs:599-613:
 //    divide when positive, else multiply). Occurrences of one id are applied
@@ -326,6 +333,7 @@ __device__ __forceinline__ uint64_t sampler_key(float v, uint32_t idx, uint32_t 
         const uint32_t pri = (__builtin_bitreverse32(idx & 255u) & 0xff000000u) | idx;
         return ((uint64_t)k << 32) | (uint32_t)~pri;
     }
+    if (v != v) return kNanKey;
     if (mode == SAMPLE_PENALTY)
         for (uint32_t c = count; c; --c) v = v > 0.0f ? v / penalty : v * penalty;
     return argmax_key(v, idx);

@@ -40,7 +40,7 @@ struct RowDev {
     int32_t nout;         // generated tokens so far (out[row][0, nout))
     int32_t done;
     int32_t eos_mode;     // EOS_* below
-    int32_t pad;
+    int32_t nan;          // set (with done) when the step's logits held a NaN under the CPU-path rules
 };
 
 // What a generated 128001 / 128009 (LLAMA3_END_OF_TEXT_ID / LLAMA3_EOT_ID) does.
@@ -135,6 +135,10 @@ __global__ void advance_kernel(AdvanceArgs a) {
         next = a.prompts[(size_t)r * a.max_seq + p + 1];
     } else if (p + 1 == c.prompt_len) {
         next = a.prompts[(size_t)r * a.max_seq + p];
+    } else if (key == kNanKey) {
+        next = a.tokens[r];   // nothing is chosen: the row stops with its NaN flag
+        c.nan = 1;
+        c.done = 1;
     } else {
         next = (int32_t)sampler_key_index(key, a.sampler->mode);
         if ((uint32_t)next >= a.vocab) next = 0;
@@ -502,6 +506,13 @@ int ensure_graph(janus_model *m, uint32_t nseq) {
     return JANUS_OK;
 }
 
+// The reference's CPU sampler panics on NaN logits (sampler.rs:191-193,
+// 397-399); here the call that ran the step returns an error.
+int nan_fail(janus_ctx *ctx, uint32_t row) {
+    return fail(ctx, JANUS_E_NAN_LOGITS,
+                "GPU returned NaN logits (batch row " + std::to_string(row) + "): no token was sampled");
+}
+
 int replay(janus_model *m, uint32_t nseq, uint32_t steps) {
     for (uint32_t s = 0; s < steps; ++s) JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(m->graphs[nseq], m->ctx->stream));
     return JANUS_OK;
@@ -534,6 +545,7 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
     }
     if (int e = janus_model_validate(m)) return e;
     if (int e = upload_sampler(m)) return e;
+    m->graph_nseq = 0;   // the rows are about to hold this loop's state, not a graph_begin's
     std::vector<int> row_req(B, -1);
     std::vector<RowDev> hrows(B);
     std::vector<int32_t> hpos(B, 0);
@@ -588,6 +600,8 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
                                             ctx->stream));
         JANUS_HIP_CHECK(ctx, hipMemcpyAsync(hpos.data(), m->d_pos, nrows * 4, hipMemcpyDeviceToHost, ctx->stream));
         JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+        for (uint32_t r = 0; r < nrows; ++r)
+            if (row_req[r] >= 0 && hrows[r].nan) return nan_fail(ctx, r);
         // retirement: finished rows hand back their tokens and free the row
         for (uint32_t r = 0; r < nrows; ++r) {
             if (row_req[r] < 0 || !hrows[r].done) continue;
@@ -953,6 +967,11 @@ int janus_model_graph_run(janus_model *m, uint32_t steps) {
             return fail(m->ctx, JANUS_E_KV_OVERFLOW, "graph: steps would exceed max_seq_len");
     if (int e = replay(m, n, steps)) return e;
     for (auto &p : m->h_pos) p += steps;
+    // a row whose step met NaN logits is stopped on the device; report it
+    RowDev rows[kMaxRows];
+    if (int e = janus_d2h(m->ctx, rows, m->d_rows, (size_t)n * sizeof(RowDev))) return e;
+    for (uint32_t r = 0; r < n; ++r)
+        if (rows[r].nan) return nan_fail(m->ctx, r);
     return JANUS_OK;
 }
 

@@ -264,6 +264,7 @@ const char *janus_status_string(int s) {
     case JANUS_E_HIP: return "hip error";
     case JANUS_E_OOM: return "out of device memory";
     case JANUS_E_NO_DEVICE: return "no device";
+    case JANUS_E_NAN_LOGITS: return "NaN logits";
     default: return "unknown status";
     }
 }

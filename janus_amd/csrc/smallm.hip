@@ -659,12 +659,13 @@ constexpr size_t pipe_lds() {
 
 template <class F, int MT, int KW, int KR>
 void launch_pipe(janus_ctx *ctx, dim3 grid, const GemmArgs &a) {
-    static bool attr_set = false;
-    if (!attr_set) {
+    // thread-safe one-time set-up (a function-local static's initialiser)
+    static const bool attr_set = [] {
         (void)hipFuncSetAttribute((const void *)gemm_pipe_kernel<F, MT, KW, KR>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
-    }
+        return true;
+    }();
+    (void)attr_set;
     constexpr size_t lds = pipe_lds<F, MT, KW, KR>();
     hipLaunchKernelGGL((gemm_pipe_kernel<F, MT, KW, KR>), grid, dim3(64 * WAVES * KW), lds, ctx->stream, a);
 }
@@ -953,14 +954,14 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
         if (int e = ensure_gemm_ws(ctx, need)) return e;
         a.ws = (float *)ctx->gemm_ws;
     }
-    static bool attr_set = false;
-    if (!attr_set) {
+    static const bool attr_set = [] {   // thread-safe one-time set-up
         (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW, SPT1, PD>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         (void)hipFuncSetAttribute((const void *)gemm_mfma_kernel<F, MT, KW, 2 * SPT1, PD>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
-    }
+        return true;
+    }();
+    (void)attr_set;
     const dim3 grid(tiles, a.ksplit), block(64 * WAVES * KW);
     // quantised weights: the cross-pass pipelined kernel for the usual pass lengths
     bool piped = false;

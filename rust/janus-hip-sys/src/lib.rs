@@ -33,6 +33,7 @@ pub const JANUS_E_TOKEN_RANGE: c_int = 5;
 pub const JANUS_E_HIP: c_int = 6;
 pub const JANUS_E_OOM: c_int = 7;
 pub const JANUS_E_NO_DEVICE: c_int = 8;
+pub const JANUS_E_NAN_LOGITS: c_int = 9;
 pub const JANUS_DT_F32: c_int = 0;
 pub const JANUS_DT_F16: c_int = 1;
 pub const JANUS_DT_Q4_0: c_int = 2;

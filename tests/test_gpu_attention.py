@@ -248,3 +248,26 @@ def test_attention_rows_matches_default_plan_at_config4_shape(engine, rows_engin
     for i in (0, 17, 31):
         sl = slice(offs[i], offs[i] + lens[i])
         _close(b[i], O.attention(q[i], k[sl], v[sl], H, KVH, D))
+
+
+def test_attention_rows_merge_ignores_stale_workspace(rows_engine):
+    """The merge of a sequence split over several workgroups reads only
+    partials written by the same launch. The first launch leaves non-finite
+    partials in workgroup 0's first slot (its first sequence has infinite V
+    and spans several workgroups); in the second, the first sequence lies
+    inside workgroup 0 (so that slot is not rewritten) while the next one is
+    split over fewer than 32 segments, whose merge has idle lanes. Every
+    output must be finite and equal the oracle."""
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng(77)
+    lens = [2000, 2000, 500]
+    q, k, v, offs, dev = _ragged_f16(rng, lens, H, KVH, D)
+    dev["vc"][: lens[0]] = float("inf")
+    _run_ragged(rows_engine, dev, lens, H, KVH, D)
+    lens = [1, 3000, 3000]
+    q, k, v, offs, dev = _ragged_f16(rng, lens, H, KVH, D)
+    got = _run_ragged(rows_engine, dev, lens, H, KVH, D)
+    assert np.isfinite(got).all()
+    for b in range(len(lens)):
+        sl = slice(offs[b], offs[b] + lens[b])
+        _close(got[b], O.attention(q[b], k[sl], v[sl], H, KVH, D))

@@ -319,3 +319,49 @@ def test_workspace_growth_keeps_captured_step():
     assert all(len(g) == 9 for g in outs[0])
     engine.sync()
     engine.close()
+
+
+def _nan_head_spec():
+    """A one-layer model whose F16 LM head holds a NaN in row 321, so every
+    step's logit 321 is NaN."""
+    s = synth.make_model(97, 256, 4, 2, 512, 1000, 1, synth.Q8_0, 1e-5, 10000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    head = [t for t in s.tensors if t.name == "output.weight"][0]
+    bits = np.array(head.data, dtype=np.uint16, copy=True).reshape(s.vocab, s.hidden)
+    bits[321, 17] = 0x7E00
+    s.tensors = [t for t in s.tensors if t.name != "output.weight"]
+    s.tensors.append(synth.Tensor("output.weight", synth.F16, s.vocab, s.hidden, bits.reshape(-1)))
+    return s
+
+
+def test_nan_logits_refused_under_cpu_sampler_rules(engine):
+    """NaN logits: the reference's CPU sampler (penalty != 1, and every batch)
+    panics (sampler.rs:191-193, 397-399), so generate, generate_batch and a
+    graph run under the penalty or plain last-max rule return
+    JANUS_E_NAN_LOGITS, and no token is chosen at that step. The GPU-argmax
+    rule (|penalty - 1| < 0.01) ignores NaN as argmax.wgsl does and follows
+    the oracle."""
+    s = _nan_head_spec()
+    prompt = _prompt(98, 5, s.vocab)
+    m = Model(engine, s, max_seq_len=32, max_batch=2)
+    m.forward([prompt[0]], [0])
+    assert np.isnan(m.logits()[0][321])
+    with pytest.raises(ops.JanusError) as ei:
+        m.generate(prompt, 4, repetition_penalty=1.15)
+    assert ei.value.status == _lib.E_NAN_LOGITS
+    with pytest.raises(ops.JanusError) as ei:
+        m.generate_batch([prompt, prompt[:3]], 4, 1.15)
+    assert ei.value.status == _lib.E_NAN_LOGITS
+    for mode, pen in ((_lib.SAMPLER_ARGMAX, 1.0), (_lib.SAMPLER_PENALTY, 1.15)):
+        m.set_sampler(mode, pen)
+        m.graph_begin([prompt[-1]], [len(prompt)])
+        with pytest.raises(ops.JanusError) as ei:
+            m.graph_run(3)
+        assert ei.value.status == _lib.E_NAN_LOGITS
+        assert m.generated(0) == []
+    # the GPU-argmax rule: NaN never wins, the stream equals the oracle's
+    got = m.generate(prompt, 6, repetition_penalty=1.0)
+    m.close()
+    assert got == O.OracleModel(s, 32).generate(prompt, 6, 1.0)
+    with pytest.raises(FloatingPointError):
+        O.OracleModel(s, 32).generate(prompt, 2, 1.15)

@@ -47,6 +47,42 @@ def test_noalloc_equals_attention_twice_second_smaller(engine, kv):
 
 
 @pytest.mark.gpu
+def test_noalloc_allocates_no_workspace():
+    """On a fresh context, calls of every split plan (row streaming, the
+    piece list, and a single sequence split over workgroups) leave the
+    context's workspaces unallocated; the regular entry point on the same
+    context then gives the same outputs (and does allocate)."""
+    from janus_amd.ops import ComputeEngine
+    eng = ComputeEngine(0)
+    try:
+        rng = np.random.default_rng(5)
+        cases = [([3000, 2500, 4096, 100], 32, 8, 128, torch.float16),   # rows plan
+                 ([3000, 2500, 900], 16, 4, 64, torch.float16),          # piece list
+                 ([6000], 32, 8, 128, torch.float32)]                    # split + merge
+        outs = []
+        for lens, H, KVH, D, kv in cases:
+            q, k, v, offs, dl = _case(rng, lens, H, KVH, D, kv)
+            B, mx = len(lens), max(lens)
+            got = torch.full((B, H * D), -7.0, device=DEV)
+            ops.compute_attention_noalloc(eng, q, k, v, got, B, 0, mx, H, KVH, D, row_base=offs, seq_lens=dl,
+                                          max_len_hint=mx)
+            torch.cuda.synchronize()
+            assert eng.workspace_bytes() == (0, 0), (lens, eng.workspace_bytes())
+            outs.append((q, k, v, offs, dl, got))
+        for (lens, H, KVH, D, kv), (q, k, v, offs, dl, got) in zip(cases, outs):
+            B, mx = len(lens), max(lens)
+            want = torch.full((B, H * D), 7.0, device=DEV)
+            ops.compute_attention(eng, q, k, v, want, B, 0, mx, H, KVH, D, row_base=offs, seq_lens=dl,
+                                  max_len_hint=mx)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), (lens, float((got - want).abs().max()))
+        assert eng.workspace_bytes()[0] > 0
+    finally:
+        eng.sync()
+        eng.close()
+
+
+@pytest.mark.gpu
 def test_noalloc_single_sequence_gqa(engine):
     """Batch 1 with a long context (the per-query-head split plan)."""
     rng = np.random.default_rng(7)
