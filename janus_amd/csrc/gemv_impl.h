@@ -131,6 +131,24 @@ __device__ __forceinline__ float dot2a(jh2 a, jh2 b, float c) {
     return r;
 }
 
+// Quantised values enter v_dot2_f32_f16 as exact binary16 integers with
+// normal encodings. The masked nibble (or byte) under the magic exponent
+// 0x6400 is 1024 + q (or 1024 + 16 q for a high nibble left in place); one
+// packed add or packed FMA then removes the 1024 (and the format's offset)
+// exactly. v_dot2_f32_f16 does not keep subnormal operands exact: with
+// q * 2^-24 encodings it returned results below the correctly rounded sum by
+// ~50 ulp on average, an error shared by every row of a product.
+__device__ __forceinline__ jh2 nib_lo(uint32_t u, uint32_t m6400, _Float16 off) {
+    const jh2 o = {off, off};
+    return as_h2((u & 0x000f000fu) | m6400) - o;   // (1024 + q) - off
+}
+__device__ __forceinline__ jh2 nib_hi(uint32_t u, uint32_t m6400, _Float16 off) {
+    const jh2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const _Float16 cb = (_Float16)(960.0f - (float)off);
+    const jh2 c = {cb, cb};
+    return __builtin_elementwise_fma(as_h2((u & 0x00f000f0u) | m6400), s16, c);   // (1024 + 16 q) / 16 + 960 - off
+}
+
 // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3): the pair order the nibble unpack produces.
 __device__ __forceinline__ void perm4(uint32_t w01, uint32_t w23, jh2 &even, jh2 &odd) {
     even = as_h2(__builtin_amdgcn_perm(w23, w01, 0x05040100u));
@@ -252,11 +270,9 @@ struct FQ4_0 {
         // sum (q-8) x = sum q x - 8 sum x
         return h2f(w.d) * fmaf(-8.0f, x.s, s0 + s1);
     }
-    // x[0..32) as pairs, and the offset term -8 sum(x) at the scale of the
-    // subnormal products (2^-24), sum(x) the binary32 sum of the same values
-    struct XH { jh2 v[16]; float s; };
-    static constexpr float XH_OFS = -8.0f / 16777216.0f;
-    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) {
+    // x[0..32) as pairs (the offset is in the unpacked weights, so no sum of x)
+    struct XH { jh2 v[16]; };
+    __device__ static XH loadx(const _Float16 *xs, const float *, int u) {
         XH r;
         const uint4 *p = (const uint4 *)(xs + u * XLayout<_Float16>::STRIDE);
 #pragma unroll
@@ -267,7 +283,6 @@ struct FQ4_0 {
             r.v[4 * i + 2] = as_h2(t.z);
             r.v[4 * i + 3] = as_h2(t.w);
         }
-        r.s = (sx16[2 * u] + sx16[2 * u + 1]) * XH_OFS;
         return r;
     }
     // register-resident x, read straight from global memory
@@ -285,33 +300,33 @@ struct FQ4_0 {
     }
     __device__ static XH loadx_g(const _Float16 *x, int u) {
         XH r;
-        r.s = (load16h_perm(x + (size_t)u * 32, r.v) + load16h_perm(x + (size_t)u * 32 + 16, r.v + 8)) * XH_OFS;
+        (void)load16h_perm(x + (size_t)u * 32, r.v);
+        (void)load16h_perm(x + (size_t)u * 32 + 16, r.v + 8);
         return r;
     }
-    // Each nibble pair is masked into binary16 subnormals with no exponent
-    // bits: q * 2^-24 (low nibbles) or 16 q * 2^-24 (high nibbles, left in
-    // place), exact, one AND per pair. v_dot2_f32_f16 takes f16 denormals
-    // (the gfx950 default mode keeps them), and q * 2^-24 * x is exact in
-    // binary32. sum (q - 8) x = sum q x - 8 sum x: the low-nibble chain s
-    // starts from -8 sum(x) * 2^-24 (x.s), the high-nibble chain t from zero,
-    // and the total is (s + t / 16) * 2^24, scaled by powers of two only.
+    // Each nibble pair becomes the exact binary16 integers q - 8 (nib_lo /
+    // nib_hi: one AND-OR and one packed add or FMA per pair), so every
+    // v_dot2_f32_f16 product is exact; the low- and high-nibble chains are
+    // added once per block and scaled by d.
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-        float s = x.s, t = 0.0f;
+        const uint32_t m = vgpr_const_6400();
+        const _Float16 off = (_Float16)1032.0f;
+        float s = 0.0f, t = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = q[i], u8 = u >> 8;
-            const jh2 a = as_h2(u & 0x000f000fu);     // (4i, 4i+2)            q * 2^-24
-            const jh2 c = as_h2(u8 & 0x000f000fu);    // (4i+1, 4i+3)
-            const jh2 b = as_h2(u & 0x00f000f0u);     // (16+4i, 16+4i+2)      16 q * 2^-24
-            const jh2 e = as_h2(u8 & 0x00f000f0u);    // (16+4i+1, 16+4i+3)
+            const jh2 a = nib_lo(u, m, off);    // (4i, 4i+2)
+            const jh2 c = nib_lo(u8, m, off);   // (4i+1, 4i+3)
+            const jh2 b = nib_hi(u, m, off);    // (16+4i, 16+4i+2)
+            const jh2 e = nib_hi(u8, m, off);   // (16+4i+1, 16+4i+3)
             // x pairs (permuted staging): v[2g] = (x[4g], x[4g+2]), v[2g+1] = (x[4g+1], x[4g+3])
-            s = i == 0 ? dot2a(a, x.v[0], s) : dot2(a, x.v[2 * i], s);
+            s = i == 0 ? dot2z(a, x.v[0]) : dot2(a, x.v[2 * i], s);
             t = i == 0 ? dot2z(b, x.v[8]) : dot2(b, x.v[8 + 2 * i], t);
             s = dot2(c, x.v[2 * i + 1], s);
             t = dot2(e, x.v[8 + 2 * i + 1], t);
         }
-        return h2f(w.d) * (fmaf(t, 0.0625f, s) * 16777216.0f);
+        return h2f(w.d) * (s + t);
     }
 };
 
@@ -338,20 +353,11 @@ struct FQ8_0 {
         return r;
     }
     using XF = FQ4_0::XF;
-    // as FQ4_0::XH with the offset term -128 sum(x) * 2^-24
     using XH = FQ4_0::XH;
     __device__ static XF loadx(const float *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
-    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) {
-        XH r = FQ4_0::loadx(xs, sx16, u);
-        r.s *= 16.0f;
-        return r;
-    }
+    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) { return FQ4_0::loadx(xs, sx16, u); }
     __device__ static XF loadx_g(const float *x, int u) { return FQ4_0::loadx_g(x, u); }
-    __device__ static XH loadx_g(const _Float16 *x, int u) {
-        XH r = FQ4_0::loadx_g(x, u);
-        r.s *= 16.0f;
-        return r;
-    }
+    __device__ static XH loadx_g(const _Float16 *x, int u) { return FQ4_0::loadx_g(x, u); }
     __device__ static float dot(const W &w, const XF &x) {
         const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
         float s0 = 0.0f, s1 = 0.0f;
@@ -366,23 +372,24 @@ struct FQ8_0 {
         }
         return h2f_q8(w.d) * fmaf(-128.0f, x.s, s0 + s1);
     }
-    // The biased bytes q + 128 (0..255) become binary16 subnormals
-    // (q + 128) * 2^-24 with a zero high byte (one v_perm_b32 per pair), as in
-    // FQ4_0: sum q x = sum (q + 128) x - 128 sum x, the chain s0 starting from
-    // -128 sum(x) * 2^-24 (x.s), s1 from zero.
+    // The biased bytes q + 128 (0..255) go under the exponent byte 0x64 with
+    // one v_perm_b32 per pair (1024 + q + 128, exact normal binary16), and a
+    // packed add of -1152 leaves the exact integers q: every v_dot2_f32_f16
+    // product is exact (see nib_lo).
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-        float s0 = x.s, s1 = 0.0f;
+        const jh2 o = {(_Float16)1152.0f, (_Float16)1152.0f};
+        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t u = q[i] ^ 0x80808080u;
-            // selector 0x0c is a zero byte: (byte 0 | 2 << 16) and (byte 1 | 3 << 16)
-            const jh2 a = as_h2(__builtin_amdgcn_perm(0u, u, 0x0c020c00u));   // (4i, 4i+2)
-            const jh2 c = as_h2(__builtin_amdgcn_perm(0u, u, 0x0c030c01u));   // (4i+1, 4i+3)
-            s0 = i == 0 ? dot2a(a, x.v[0], s0) : dot2(a, x.v[2 * i], s0);
+            // bytes 4-7 of the pool are 0x64: (byte 0 | 0x64 << 8, byte 2 | 0x64 << 8) and bytes 1, 3
+            const jh2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04020400u)) - o;   // (4i, 4i+2)
+            const jh2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030401u)) - o;   // (4i+1, 4i+3)
+            s0 = i == 0 ? dot2z(a, x.v[0]) : dot2(a, x.v[2 * i], s0);
             s1 = i == 0 ? dot2z(c, x.v[1]) : dot2(c, x.v[2 * i + 1], s1);
         }
-        return h2f_q8(w.d) * ((s0 + s1) * 16777216.0f);
+        return h2f_q8(w.d) * (s0 + s1);
     }
 };
 
@@ -531,25 +538,26 @@ struct FQ4_K {
         }
         return finish(w, x, l0 + l1, h0 + h1);
     }
-    // Nibbles as binary16 subnormals q * 2^-24 (low) and 16 q * 2^-24 (high,
-    // left in place), one AND per pair (see FQ4_0); the sums scale back by
-    // powers of two.
+    // Nibbles as the exact binary16 integers q (nib_lo / nib_hi with no
+    // offset, see FQ4_0).
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        const uint32_t m = vgpr_const_6400();
+        const _Float16 off = (_Float16)1024.0f;
         float l = 0.0f, h = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = q[i], u8 = u >> 8;
-            const jh2 a = as_h2(u & 0x000f000fu);
-            const jh2 c = as_h2(u8 & 0x000f000fu);
-            const jh2 b = as_h2(u & 0x00f000f0u);
-            const jh2 e = as_h2(u8 & 0x00f000f0u);
+            const jh2 a = nib_lo(u, m, off);
+            const jh2 c = nib_lo(u8, m, off);
+            const jh2 b = nib_hi(u, m, off);
+            const jh2 e = nib_hi(u8, m, off);
             l = i == 0 ? dot2z(a, x.lo[0]) : dot2(a, x.lo[2 * i], l);
             h = i == 0 ? dot2z(b, x.hi[0]) : dot2(b, x.hi[2 * i], h);
             l = dot2(c, x.lo[2 * i + 1], l);
             h = dot2(e, x.hi[2 * i + 1], h);
         }
-        return finish(w, x, l * 16777216.0f, h * 1048576.0f);
+        return finish(w, x, l, h);
     }
 };
 
@@ -613,22 +621,25 @@ struct FQ5_K : FQ4_K {
         return finish(w, x, l0 + l1, h0 + h1);
     }
     __device__ static float dot(const W &w, const XH &x) {
+        const uint32_t m = vgpr_const_6400();
+        const jh2 o = {(_Float16)1024.0f, (_Float16)1024.0f};
         float l = 0.0f, h = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint32_t lo, hi;
             q5(w, i, lo, hi);
-            // bytes 0, 2 and 1, 3 of each word as binary16 subnormals q * 2^-24 (q <= 31)
-            const jh2 a = as_h2(lo & 0x001f001fu);
-            const jh2 c = as_h2((lo >> 8) & 0x001f001fu);
-            const jh2 b = as_h2(hi & 0x001f001fu);
-            const jh2 e = as_h2((hi >> 8) & 0x001f001fu);
+            // bytes 0, 2 and 1, 3 of each word as the exact binary16 integers
+            // q <= 31: (1024 + q) - 1024 (see nib_lo)
+            const jh2 a = as_h2((lo & 0x001f001fu) | m) - o;
+            const jh2 c = as_h2(((lo >> 8) & 0x001f001fu) | m) - o;
+            const jh2 b = as_h2((hi & 0x001f001fu) | m) - o;
+            const jh2 e = as_h2(((hi >> 8) & 0x001f001fu) | m) - o;
             l = i == 0 ? dot2z(a, x.lo[0]) : dot2(a, x.lo[2 * i], l);
             h = i == 0 ? dot2z(b, x.hi[0]) : dot2(b, x.hi[2 * i], h);
             l = dot2(c, x.lo[2 * i + 1], l);
             h = dot2(e, x.hi[2 * i + 1], h);
         }
-        return finish(w, x, l * 16777216.0f, h * 16777216.0f);
+        return finish(w, x, l, h);
     }
 };
 

@@ -42,6 +42,7 @@ struct janus_ctx {
     // whole cache rows through LDS, one workgroup per CU (JANUS_ATTN_ROWS:
     // 0 never, 1 whenever the shape allows, unset: planned)
     int attn_rows = -1;
+    bool fused_step = true;          // JANUS_FUSED=0: models take the per-operator step (A/B and parity probes)
     // wavefronts per workgroup of the per-query-head attention launch (short
     // contexts, few sequences): 4, 8 or 16 (JANUS_ATTN_QH_NW; 0: planned)
     uint32_t attn_qh_nw = 0;

@@ -310,7 +310,9 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
 
 bool use_fused1(const janus_model *m, uint32_t nseq) {
     // the fused norms stage x in registers: hidden <= 8192
-    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready || m->cfg.hidden > 8192) return false;
+    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready || m->cfg.hidden > 8192 ||
+        !m->ctx->fused_step)
+        return false;
     for (const auto &L : m->layers)
         if (!L.qkv || !L.gu) return false;
     return true;
@@ -320,7 +322,8 @@ bool use_fused1(const janus_model *m, uint32_t nseq) {
 // every layer on the MFMA path and rows the one-workgroup norm can hold.
 bool fused_batch_ok(const janus_model *m) {
     const janus_model_config &c = m->cfg;
-    if (c.act_dtype != JANUS_DT_F16 || c.max_batch < 2 || !m->fused_ready || !resnorm_supported(c.hidden))
+    if (c.act_dtype != JANUS_DT_F16 || c.max_batch < 2 || !m->fused_ready || !resnorm_supported(c.hidden) ||
+        !m->ctx->fused_step)
         return false;
     for (const auto &L : m->layers)
         if (!L.qkv || !L.gu || !mfma_gemm_supported(JANUS_DT_F16, L.qkv) || !mfma_gemm_supported(JANUS_DT_F16, L.gu) ||

@@ -346,6 +346,7 @@ int janus_create(int hip_device, janus_ctx **out) {
         if (!std::strcmp(k, "0")) ctx->attn_rows = 0;
         else if (!std::strcmp(k, "1")) ctx->attn_rows = 1;
     }
+    if (const char *k = std::getenv("JANUS_FUSED")) ctx->fused_step = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_ATTN_TASK")) {
         const long v = std::strtol(k, nullptr, 10);
         if (v >= 16 && v <= 4096) ctx->attn_task = (uint32_t)v;

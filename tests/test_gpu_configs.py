@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 import torch
 
+from greedy import assert_same_or_near_tie
 from janus_amd import _lib, ops, synth
 from janus_amd.model import Model
 from oracle import oracle as O
@@ -135,17 +136,79 @@ def test_config5_lm_head_m32_matches_f64(engine):
     assert ratio <= 1.0, ratio
 
 
-def test_config5_32_sequence_step_equals_single_runs(engine):
+@pytest.fixture(scope="module")
+def llama3_full():
+    """The headline workload's model (bench.py): Llama-3-8B architecture, 32
+    layers, Q4_0 blocks, F16 embeddings and LM head, vocab 128256."""
+    return synth.make_model(7, 4096, 32, 8, 14336, 128256, 32, synth.Q4_0, 1e-5, 500000.0,
+                            embed_type=synth.F16, head_type=synth.F16)
+
+
+def _eager_greedy(m, prompt, steps, penalty, ref_logits):
+    """Eager decode on the GPU with the oracle's sampler on the GPU's logits;
+    returns the tokens and, per step, the logits' error against ref_logits
+    (meaningful while the streams agree)."""
+    for p, t in enumerate(prompt):
+        m.forward([t], [p])
+    last, pos, gen, errs = prompt[-1], len(prompt), [], []
+    for i in range(steps):
+        m.forward([last], [pos])
+        lg = m.logits()[0]
+        if i < len(ref_logits):
+            errs.append(_rel_err(lg, ref_logits[i]))
+            print(f"step {i}: logits {errs[-1]:.2e} against the oracle", flush=True)
+        last = O.greedy_sample(lg, gen, penalty)
+        gen.append(last)
+        pos += 1
+    return gen, errs
+
+
+def test_headline_model_reference_dtypes_tokens_and_logits(engine, llama3_full):
+    """The full 32-layer headline model on the reference's dtypes (f32
+    activations into the products, f32 KV) against the oracle: 16 greedy
+    tokens with the default sampler (penalty 1.15) identical, eagerly and in
+    the device loop, and the logits within 2e-3 at every step
+    (generation.rs:129-323, sampler.rs:146-209)."""
+    spec = llama3_full
+    prompt = np.random.default_rng(8).integers(0, spec.vocab, 8).tolist()
+    want, wl = O.OracleModel(spec, 32).generate(prompt, 16, 1.15, return_logits=True)
+    m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F32, act_dtype=_lib.DT_F32)
+    gen, errs = _eager_greedy(m, prompt, 16, 1.15, wl)
+    dev = m.generate(prompt, 16, repetition_penalty=1.15)
+    m.close()
+    assert gen == want
+    assert dev == want
+    assert max(errs) <= REL, errs
+
+
+def test_headline_model_binary16_path_tokens(engine, llama3_full):
+    """The full 32-layer headline model on the bench path (binary16
+    activations and KV, fused single-sequence step, captured device loop)
+    against the oracle's binary16 mode: 16 greedy tokens identical, or parted
+    only at a certified near tie; the eager step's logits within 2e-3 while
+    the streams agree."""
+    spec = llama3_full
+    prompt = np.random.default_rng(9).integers(0, spec.vocab, 8).tolist()
+    want, wl = O.OracleModel(spec, 32, kv_f16=True, act_f16=True).generate(prompt, 16, 1.15, return_logits=True)
+    m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    dev = m.generate(prompt, 16, repetition_penalty=1.15)
+    gen, errs = _eager_greedy(m, prompt, 16, 1.15, wl)
+    m.close()
+    assert len(dev) == 16
+    assert gen == dev
+    split = assert_same_or_near_tie(dev, want, wl, 1.15)
+    assert max(errs[: split + 1]) <= REL, errs
+
+
+def test_config5_32_sequence_step_equals_single_runs(engine, llama3_full):
     """One full-dimension ragged step: 32 sequences at positions U[256, 4096]
     over random fp16 caches, on the fused batched path (MFMA products), against
     the same sequences stepped alone (GEMV path) in their own KV slots."""
-    spec = synth.make_model(7, 4096, 32, 8, 14336, 128256, 32, synth.Q4_0, 1e-5, 500000.0,
-                            embed_type=synth.F16, head_type=synth.F16)
+    spec = llama3_full
     rng = np.random.default_rng(5)
     lens = rng.integers(256, 4097, 32)
     max_seq = int(lens.max()) + 1
     m = Model(engine, spec, max_seq_len=max_seq, max_batch=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
-    del spec
     shape = (32, 32 * max_seq, 8, 128)
     g = torch.Generator(device=DEV).manual_seed(5)
     kc = torch.randn(shape, device=DEV, dtype=torch.float16, generator=g)
@@ -171,29 +234,23 @@ def c5_two_layers():
 def test_config5_two_layers_logits_match_oracle(engine, c5_two_layers):
     """The binary16-activation step against the oracle in its
     binary16-activation mode (activations rounded where this path stores them),
-    every step. Random models have the odd step that amplifies rounding-level
-    differences (here step 6: the oracle's own f16- and f32-KV variants differ
-    by 4e-3 there, against 4e-6 at the other steps). The bound therefore grows
-    with the sensitivity the oracle measures on itself: 2e-3 plus three times the
-    difference between its two KV roundings, and at most one step may need
-    more than the plain 2e-3."""
+    every step, at the plain 2e-3 bound. Step 6 of this prompt is the
+    sensitive one (the oracle's own f16- and f32-KV variants differ by 2.7e-3
+    there): it needs products whose rounding errors are independent across
+    rows, which the binary16 products give since their quantised operands are
+    exact normal binary16 integers."""
     spec = c5_two_layers
     prompt = np.random.default_rng(43).integers(0, spec.vocab, 10).tolist()
     ref = O.OracleModel(spec, 64, kv_f16=True, act_f16=True)
-    probe = O.OracleModel(spec, 64, kv_f16=False, act_f16=True)
     m = Model(engine, spec, max_seq_len=64, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
-    over = []
+    errs = []
     for p, t in enumerate(prompt):
         want = ref.forward(t, p)
-        sens = _rel_err(probe.forward(t, p), want)
         m.forward([t], [p])
-        err = _rel_err(m.logits()[0], want)
-        print(f"step {p}: {err:.2e} against the oracle, its KV-rounding sensitivity {sens:.2e}", flush=True)
-        assert err <= REL + 3 * sens, (p, err, sens)
-        if err > REL:
-            over.append(p)
+        errs.append(_rel_err(m.logits()[0], want))
+        print(f"step {p}: {errs[-1]:.2e} against the oracle", flush=True)
     m.close()
-    assert len(over) <= 1, over
+    assert max(errs) <= REL, errs
 
 
 def test_config5_two_layers_greedy_tokens(engine, c5_two_layers):
@@ -204,3 +261,30 @@ def test_config5_two_layers_greedy_tokens(engine, c5_two_layers):
     got = m.generate(prompt, 12, 1.15)
     m.close()
     assert got == want
+
+
+def _f32_parity(engine, spec, seed, steps=8):
+    """Reference dtypes (f32 activations, f32 KV) against the f32 oracle:
+    logits within 2e-3 at every prompt and decode step, greedy tokens
+    (penalty 1.15) identical."""
+    prompt = np.random.default_rng(seed).integers(0, spec.vocab, 8).tolist()
+    ref = O.OracleModel(spec, 32)
+    m = Model(engine, spec, max_seq_len=32, kv_dtype=_lib.DT_F32, act_dtype=_lib.DT_F32)
+    errs = []
+    for p, t in enumerate(prompt):
+        want = ref.forward(t, p)
+        m.forward([t], [p])
+        errs.append(_rel_err(m.logits()[0], want))
+    want_toks = ref.generate(prompt, steps, 1.15)
+    got = m.generate(prompt, steps, repetition_penalty=1.15)
+    m.close()
+    assert max(errs) <= REL, errs
+    assert got == want_toks
+
+
+def test_config3_two_layers_reference_dtypes(engine, c3_two_layers):
+    _f32_parity(engine, c3_two_layers, 33)
+
+
+def test_config5_two_layers_reference_dtypes(engine, c5_two_layers):
+    _f32_parity(engine, c5_two_layers, 45)
