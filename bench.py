@@ -386,7 +386,7 @@ def main() -> int:
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs1pen", "bs32", "copy", "attn", "c3", "gemm",
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs1pen", "bs1ref", "bs32", "copy", "attn", "c3", "gemm",
                                        "kquant"],
                     default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
@@ -480,6 +480,11 @@ def main() -> int:
     if args.only == "bs32":
         ms32, ctx_sum = decode_bs32(engine, spec, args.steps, args.warmup)
         log(f"bs=32 ragged: {ms32 / args.steps:.3f} ms/step, {32 * args.steps / (ms32 / 1e3):.1f} tok/s")
+        return 0
+    if args.only == "bs1ref":
+        nref = max(10, args.steps // 4)
+        msr, _ = decode_bs1(engine, spec, nref, args.warmup, f32=True)
+        log(f"bs=1 reference dtypes: {msr / nref:.3f} ms/token")
         return 0
     if args.only == "bs1pen":
         msp, _ = decode_bs1(engine, spec, args.steps, args.warmup, penalty=1.15, trials=HEADLINE_TRIALS)

@@ -33,7 +33,7 @@ RunFn runner(const janus_weight *w, uint32_t &units) {
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
                        void *vc, int kv_f16, const float *rope, const int32_t *d_pos, const int32_t *d_rowbase,
                        uint32_t q_pairs, uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row, const float *gamma,
-                       float eps) {
+                       float eps, int x32) {
     GemvArgs a;
     std::memset(&a, 0, sizeof(a));
     a.gamma = gamma;
@@ -64,13 +64,14 @@ int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int
     if (w->type == JANUS_DT_F16 && a.units == 0)
         return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: F16 rows need k % 8 == 0");
     bool done = false;
-    const int e = run(ctx, a, GEMV_PAIR | (norm ? GEMV_NORM : 0), JANUS_DT_F16, &done);
+    const int e = run(ctx, a, GEMV_PAIR | (norm ? GEMV_NORM : 0) | (x32 ? GEMV_X32 : 0),
+                      x32 ? JANUS_DT_F32 : JANUS_DT_F16, &done);
     if (!e && !done) return fail(ctx, JANUS_E_INVALID_DIM, "paired gemv: row too long");
     return e;
 }
 
 int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
-                       unsigned long long *best, const uint32_t *counts, const SamplerDev *sampler) {
+                       unsigned long long *best, const uint32_t *counts, const SamplerDev *sampler, int x32) {
     GemvArgs a;
     std::memset(&a, 0, sizeof(a));
     a.w.qs = w->qs;
@@ -91,7 +92,7 @@ int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float
     if (w->type == JANUS_DT_F16 && a.units == 0)
         return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: F16 rows need k % 8 == 0");
     bool done = false;
-    const int e = run(ctx, a, GEMV_NORM, JANUS_DT_F32, &done);
+    const int e = run(ctx, a, GEMV_NORM | (x32 ? GEMV_X32 : 0), JANUS_DT_F32, &done);
     if (!e && !done) return fail(ctx, JANUS_E_INVALID_DIM, "normed gemv: row too long");
     return e;
 }

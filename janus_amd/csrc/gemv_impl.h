@@ -72,7 +72,8 @@ struct GemvArgs {
 
 // kinds of product: plain (x as given), or x RMS-normalised on staging
 // (GEMV_NORM), with paired-row epilogues (GEMV_PAIR, two rows per step)
-enum { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_PAIR = 2 };
+// (GEMV_X32: x staged as binary32, the reference's activation dtype)
+enum { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_PAIR = 2, GEMV_X32 = 4 };
 
 // One launch of the product `a` for one weight format (the format's own
 // translation unit); *done = false when no kernel covers the row length.
@@ -966,7 +967,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
                 // would hoist every unit's read out of the group loop, keeping
                 // them all live (spills on long rows); an opaque index keeps
                 // each read next to its use
-                if constexpr (F::XREREAD) asm volatile("" : "+v"(u));
+                if constexpr (F::XREREAD || sizeof(XT) == 4) asm volatile("" : "+v"(u));
                 xv = F::loadx(xs, sx16, u);
             } else {
                 xv = xr[i];
@@ -976,7 +977,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
                 const float d = F::dot(w[i][r], xv);
                 acc[r] = ok[i] ? acc[r] + d : acc[r];
             }
-            if constexpr (XMODE == 2 && F::XREREAD) __builtin_amdgcn_sched_barrier(0);
+            if constexpr (XMODE == 2 && (F::XREREAD || sizeof(XT) == 4)) __builtin_amdgcn_sched_barrier(0);
         }
         int ridx;
         float s = reduce_wave_rows<R>(acc, lane, ridx);
@@ -1156,16 +1157,15 @@ __device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, uint32_t nt, _Floa
     __syncthreads();
     float tot = 0.0f;
     for (uint32_t w = 0; w < (nt >> 6); ++w) tot += red[w];
-    // x * (1 / rms) instead of x / rms: within one ulp, and the staged value
-    // is rounded to binary16 right after
-    const float inv = 1.0f / sqrtf(tot / (float)k + eps);
+    // (x / rms) * gamma, the reference's formula (activations.wgsl:128)
+    const float rms = sqrtf(tot / (float)k + eps);
 #pragma unroll
     for (int j = 0; j < 4 * MAXG; ++j) {
         if (nt * j >= nslot) break;   // uniform: no slot of this round is staged
         const uint32_t sl = threadIdx.x + nt * j, e0 = 4 * sl;
         _Float16 hv[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) hv[t] = (_Float16)((r.v[j][t] * inv) * r.gm[j][t]);
+        for (int t = 0; t < 4; ++t) hv[t] = (_Float16)((r.v[j][t] / rms) * r.gm[j][t]);
         // the group's sum of its binary16 values: lane, then lane pairs of the quad
         float q = (((float)hv[0] + (float)hv[1]) + (float)hv[2]) + (float)hv[3];
         q += dpp_f<0xb1>(q);   // quad_perm [1,0,3,2]
@@ -1174,6 +1174,46 @@ __device__ void stage_x16_norm(NormRegs<MAXG> &r, uint32_t k, uint32_t nt, _Floa
             if ((threadIdx.x & 3) == 0) sx16[sl >> 2] = q;
             const jh4 o = PERM ? (jh4){hv[0], hv[2], hv[1], hv[3]} : (jh4){hv[0], hv[1], hv[2], hv[3]};
             *(jh4 *)(xs + (e0 / 32) * XLayout<_Float16>::STRIDE + (e0 % 32)) = o;
+        }
+    }
+}
+
+// The same staging in binary32 (the reference's dtype): (x / rms) * gamma
+// stored unrounded in the f32 LDS layout (natural element order), with the
+// 16-element sums beside it.
+template <int MAXG>
+__device__ void stage_x32_norm(NormRegs<MAXG> &r, uint32_t k, uint32_t nt, float *xs, float *sx16, float eps,
+                               float *red) {
+    const uint32_t nslot = 4 * ((k + 15) / 16);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4 * MAXG; ++j) {
+        if (nt * j >= nslot) break;
+        if (4 * (threadIdx.x + nt * j) >= k) r.v[j] = (jf4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ss = fmaf(r.v[j][t], r.v[j][t], ss);
+    }
+    float sv[1] = {ss};
+    int ridx;
+    ss = reduce_wave_rows<1>(sv, threadIdx.x & 63, ridx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (uint32_t w = 0; w < (nt >> 6); ++w) tot += red[w];
+    const float rms = sqrtf(tot / (float)k + eps);
+#pragma unroll
+    for (int j = 0; j < 4 * MAXG; ++j) {
+        if (nt * j >= nslot) break;
+        const uint32_t sl = threadIdx.x + nt * j, e0 = 4 * sl;
+        jf4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = (r.v[j][t] / rms) * r.gm[j][t];
+        float q = ((v[0] + v[1]) + v[2]) + v[3];
+        q += dpp_f<0xb1>(q);   // quad_perm [1,0,3,2]
+        q += dpp_f<0x4e>(q);   // quad_perm [2,3,0,1]
+        if (sl < nslot) {
+            if ((threadIdx.x & 3) == 0) sx16[sl >> 2] = q;
+            *(jf4 *)(xs + (e0 / 32) * XLayout<float>::STRIDE + (e0 % 32)) = v;
         }
     }
 }
@@ -1340,6 +1380,36 @@ __global__ __launch_bounds__((lds_max_threads<F, BPL>())) void gemv_lds_kernel(G
         gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
 }
 
+// The LDS-staged product on binary32 x (the reference's dtype; the fused
+// single-sequence step with f32 activations): x, or its RMSNorm (requested
+// before the weights), is staged once per workgroup as f32 and each unit's
+// 32 values are read from LDS next to their use (an f32 unit is 32 VGPRs).
+// 512-thread workgroups; the format's binary32 dot (exact integer weights,
+// fp32 FMAs) as in the register kernel.
+template <class F, int BPL, int R, bool NORM>
+__global__ __launch_bounds__(512) void gemv_lds32_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    float *xs = (float *)smem;
+    float *sx16 = (float *)(smem + ((nblk * XLayout<float>::STRIDE * 4 + 15) & ~15u));
+    float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
+    NormRegs<NORM_MAXG> nr;
+    const uint32_t nt = a.threads;
+    auto pre = [&]() {
+        if constexpr (NORM) norm_load<NORM_MAXG>((const float *)a.x, a.gamma, a.k, nt, nr);
+    };
+    auto stage = [&]() {
+        if constexpr (NORM) stage_x32_norm<NORM_MAXG>(nr, a.k, nt, xs, sx16, a.eps, red);
+        else stage_x<float, float, false>((const float *)a.x, a.k, xs, sx16, (int)nt);
+        __syncthreads();
+    };
+    constexpr bool DB = BPL <= 4;
+    if (a.units == 64u * BPL)
+        gemv_reg_body<F, float, BPL, R, true, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+    else
+        gemv_reg_body<F, float, BPL, R, false, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+}
+
 // Generic fallback for F16 weights whose k is not a multiple of 8: one
 // wavefront per row, scalar loads (the tiny-model ffn_down case, k = 688).
 template <typename XIN>
@@ -1503,6 +1573,74 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     return JANUS_OK;
 }
 
+// binary32 x: persistent grid of 512-thread workgroups (resident ones only)
+template <class F, int BPL, int R>
+int launch_lds32(janus_ctx *ctx, const GemvArgs &a, bool norm) {
+    const int threads = 512, wg_waves = 8;
+    const uint32_t groups = (a.n + R - 1) / R;
+    const uint32_t nblk = (a.k + XB - 1) / XB;
+    const size_t lds = ((nblk * XLayout<float>::STRIDE * 4 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
+    if (lds > 160 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for f32 LDS staging");
+    const void *kern = norm ? (const void *)gemv_lds32_kernel<F, BPL, R, true> : (const void *)gemv_lds32_kernel<F, BPL, R, false>;
+    static const bool attr_set = [] {   // > 64 KiB of dynamic LDS for long rows; thread-safe one-time set-up
+        (void)hipFuncSetAttribute((const void *)gemv_lds32_kernel<F, BPL, R, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute((const void *)gemv_lds32_kernel<F, BPL, R, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        return true;
+    }();
+    (void)attr_set;
+    static std::atomic<int> per_cu[2][41] = {};   // [norm][LDS size in 4 KB steps], relaxed
+    const size_t lds_step = (lds + 4095) / 4096;
+    std::atomic<int> &occ_cache = per_cu[norm ? 1 : 0][lds_step];
+    int occ = occ_cache.load(std::memory_order_relaxed);
+    if (occ == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, lds_step * 4096) != hipSuccess || nb < 1)
+            nb = 1;
+        occ = nb;
+        occ_cache.store(occ, std::memory_order_relaxed);
+    }
+    const int wg_cap = (int)ctx->gemv_lds_wpc / wg_waves;
+    int pc = occ < wg_cap ? occ : wg_cap;
+    if (pc < 1) pc = 1;
+    uint32_t blocks = (groups + wg_waves - 1) / wg_waves;
+    const uint32_t cap = (uint32_t)ctx->num_cus * pc;
+    if (blocks > cap) blocks = cap;
+    GemvArgs b = a;
+    b.threads = (uint32_t)threads;
+    if (norm) hipLaunchKernelGGL((gemv_lds32_kernel<F, BPL, R, true>), dim3(blocks), dim3(threads), lds, ctx->stream, b);
+    else hipLaunchKernelGGL((gemv_lds32_kernel<F, BPL, R, false>), dim3(blocks), dim3(threads), lds, ctx->stream, b);
+    JANUS_LAUNCH_CHECK(ctx);
+    return JANUS_OK;
+}
+
+template <class F>
+int launch_lds32_fmt(janus_ctx *ctx, const GemvArgs &a, bool norm, bool pair, bool &done) {
+    const int bpl = (int)((a.units + 63) / 64);
+    done = bpl <= 8;
+    if (!done) return JANUS_OK;
+    if (pair) {
+        switch (bpl) {
+        case 1: return launch_lds32<F, 1, 2>(ctx, a, norm);
+        case 2: return launch_lds32<F, 2, 2>(ctx, a, norm);
+        case 3: return launch_lds32<F, 3, 2>(ctx, a, norm);
+        case 4: return launch_lds32<F, 4, 2>(ctx, a, norm);
+        default: done = false; return JANUS_OK;
+        }
+    }
+    switch (bpl) {
+    case 1: return launch_lds32<F, 1, 4>(ctx, a, norm);
+    case 2: return launch_lds32<F, 2, 1>(ctx, a, norm);
+    case 3: return launch_lds32<F, 3, 1>(ctx, a, norm);
+    case 4: return launch_lds32<F, 4, 1>(ctx, a, norm);
+    case 5: return launch_lds32<F, 5, 1>(ctx, a, norm);
+    case 6: return launch_lds32<F, 6, 1>(ctx, a, norm);
+    case 7: return launch_lds32<F, 7, 1>(ctx, a, norm);
+    default: return launch_lds32<F, 8, 1>(ctx, a, norm);
+    }
+}
+
 // Units per lane = ceil(units / 64), up to 8. Rows per wavefront step: four
 // at one unit per lane, one at two (each wavefront's last row group, whose
 // arithmetic runs after the stream has ended, is half as long: Q4_0
@@ -1551,6 +1689,11 @@ int launch_gemv(janus_ctx *ctx, GemvArgs a, int x_dt) {
         e = launch_lds_fmt<F>(ctx, a, false, false, done);
         if (done || e) return e;
     }
+    // binary32 x: the f32 LDS staging, once per workgroup
+    if (x_dt == JANUS_DT_F32 && ctx->gemv_lds && a.units >= 64) {
+        e = launch_lds32_fmt<F>(ctx, a, false, false, done);
+        if (done || e) return e;
+    }
     if (x_dt == JANUS_DT_F16) e = launch_reg_fmt<F, _Float16>(ctx, a, done);
     else e = launch_reg_fmt<F, float>(ctx, a, done);
     if (done || e) return e;
@@ -1580,6 +1723,8 @@ int gemv_run(janus_ctx *ctx, const GemvArgs &a, int mode, int x_dt, bool *done) 
         }
     }
     if (mode == janus::GEMV_PLAIN) return launch_gemv<F>(ctx, a, x_dt);
+    if (mode & janus::GEMV_X32)
+        return launch_lds32_fmt<F>(ctx, a, (mode & janus::GEMV_NORM) != 0, (mode & janus::GEMV_PAIR) != 0, *done);
     return launch_lds_fmt<F>(ctx, a, (mode & janus::GEMV_NORM) != 0, (mode & janus::GEMV_PAIR) != 0, *done);
 }
 

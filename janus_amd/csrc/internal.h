@@ -143,18 +143,20 @@ int gemv_dispatch(janus_ctx *ctx, const void *x, int x_dt, const janus_weight *w
 // Paired-row M = 1 products: epi 0 = fused QKV with RoPE and KV append (q
 // rotated into y, f32; K/V land in cache row rowbase[0] + pos[0], rowbase may
 // be null for 0), epi 1 = fused gate/up with SwiGLU into y. x is f16, or,
-// with gamma set, the f32 residual stream RMS-normalised in the kernel.
+// with gamma set, the f32 residual stream RMS-normalised in the kernel. x32:
+// the products read binary32 x (f32 x, or its RMSNorm kept in f32: the
+// reference's dtype) instead of binary16.
 int gemv_pair_dispatch(janus_ctx *ctx, const void *x, const janus_weight *w, int epi, void *y, int y_f16, void *kc,
                        void *vc, int kv_f16, const float *rope, const int32_t *d_pos, const int32_t *d_rowbase,
                        uint32_t q_pairs, uint32_t k_pairs, uint32_t half_hd, uint32_t kv_row,
-                       const float *gamma = nullptr, float eps = 0.0f);
+                       const float *gamma = nullptr, float eps = 0.0f, int x32 = 0);
 // M = 1 product of RMSNorm(x, gamma, eps) (x f32) into y (f32). With best
 // set, the outputs are also folded into *best as the running maximum of
 // sampler_key (counts: the row's occurrence counts of generated tokens, or
 // null); *best must be 0 before the launch.
 int gemv_norm_dispatch(janus_ctx *ctx, const float *x, const float *gamma, float eps, const janus_weight *w, float *y,
                        unsigned long long *best, const uint32_t *counts = nullptr,
-                       const SamplerDev *sampler = nullptr);
+                       const SamplerDev *sampler = nullptr, int x32 = 0);
 // Row layout of an uploaded weight (bytes of quants, binary16 scales per row).
 size_t weight_qs_row_bytes(int type, uint32_t k);
 size_t weight_sc_row_elems(int type, uint32_t k);

@@ -271,7 +271,7 @@ bool can_fold_head(const janus_model *m) {
     return (w->k / 8 + 63) / 64 <= 8;
 }
 
-// Single-sequence step over the fused weights (f16 activations): per layer
+// Single-sequence step over the fused weights (binary16 or binary32 activations): per layer
 // QKV (with the attention RMSNorm in its prologue and RoPE + KV append in its
 // epilogue), attention, o-proj + residual, gate/up (FFN RMSNorm prologue,
 // SwiGLU epilogue), down-proj + residual; the final RMSNorm runs in the LM
@@ -282,6 +282,7 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
     const janus_model_config &c = m->cfg;
     const uint32_t kvd = c.kv_heads * c.head_dim, half = c.head_dim / 2;
     const int kv16 = c.kv_dtype == JANUS_DT_F16;
+    const int f32 = c.act_dtype == JANUS_DT_F32;   // the reference's dtype: every product reads binary32 x
     int e;
     if ((e = embed_launch(ctx, m->tok_embd, h_ids, d_ids, 1, m->hidden))) return e;
     for (uint32_t l = 0; l < c.layers; ++l) {
@@ -289,30 +290,29 @@ int forward_fused1(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, 
         void *kc = (uint8_t *)m->kcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
         void *vc = (uint8_t *)m->vcache + (size_t)l * m->layer_kv_elems * kv_elem_bytes(c.kv_dtype);
         if ((e = gemv_pair_dispatch(ctx, m->hidden, L.qkv, 0, m->q, 0, kc, vc, kv16, m->rope, m->d_pos, m->d_rowbase,
-                                    c.heads * half, c.kv_heads * half, half, kvd, L.attn_norm, c.rms_eps)))
+                                    c.heads * half, c.kv_heads * half, half, kvd, L.attn_norm, c.rms_eps, f32)))
             return e;
-        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, m->attn16, 1, c.heads, c.kv_heads, c.head_dim, 0,
+        void *att = f32 ? (void *)m->attn : m->attn16;
+        if ((e = attention_launch(ctx, m->q, kc, vc, c.kv_dtype, att, 1, c.heads, c.kv_heads, c.head_dim, 0,
                                   c.max_seq_len, m->d_rowbase, m->d_lens, max_len, 1.0f / sqrtf((float)c.head_dim),
-                                  1)))
+                                  f32 ? 0 : 1)))
             return e;
-        if ((e = gemm_dispatch(ctx, m->attn16, JANUS_DT_F16, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
-        if ((e = gemv_pair_dispatch(ctx, m->h1, L.gu, 1, m->act, 1, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0,
-                                    0, 0, 0, L.ffn_norm, c.rms_eps)))
+        if ((e = gemm_dispatch(ctx, att, c.act_dtype, L.o, m->h1, JANUS_DT_F32, 1, m->hidden))) return e;
+        if ((e = gemv_pair_dispatch(ctx, m->h1, L.gu, 1, m->act, f32 ? 0 : 1, nullptr, nullptr, 0, nullptr, nullptr,
+                                    nullptr, 0, 0, 0, 0, L.ffn_norm, c.rms_eps, f32)))
             return e;
-        if ((e = gemm_dispatch(ctx, m->act, JANUS_DT_F16, L.down, m->hidden, JANUS_DT_F32, 1, m->h1))) return e;
+        if ((e = gemm_dispatch(ctx, m->act, c.act_dtype, L.down, m->hidden, JANUS_DT_F32, 1, m->h1))) return e;
     }
     if (can_fold_head(m))
         return gemv_norm_dispatch(ctx, m->hidden, m->out_norm, c.rms_eps, m->lm_head, m->logits,
-                                  fold_sample ? m->d_best : nullptr, m->d_counts, m->d_sampler);
-    if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, JANUS_DT_F16, m->out_norm, 1, c.hidden, c.rms_eps))) return e;
-    return gemm_dispatch(ctx, m->xn, JANUS_DT_F16, m->lm_head, m->logits, JANUS_DT_F32, 1, nullptr);
+                                  fold_sample ? m->d_best : nullptr, m->d_counts, m->d_sampler, f32);
+    if ((e = rmsnorm_launch(ctx, m->hidden, m->xn, c.act_dtype, m->out_norm, 1, c.hidden, c.rms_eps))) return e;
+    return gemm_dispatch(ctx, m->xn, c.act_dtype, m->lm_head, m->logits, JANUS_DT_F32, 1, nullptr);
 }
 
 bool use_fused1(const janus_model *m, uint32_t nseq) {
     // the fused norms stage x in registers: hidden <= 8192
-    if (nseq != 1 || m->cfg.act_dtype != JANUS_DT_F16 || !m->fused_ready || m->cfg.hidden > 8192 ||
-        !m->ctx->fused_step)
-        return false;
+    if (nseq != 1 || !m->fused_ready || m->cfg.hidden > 8192 || !m->ctx->fused_step) return false;
     for (const auto &L : m->layers)
         if (!L.qkv || !L.gu) return false;
     return true;
@@ -797,8 +797,8 @@ int janus_model_validate(janus_model *m) {
         if (!L.attn_norm || !L.ffn_norm || !L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down)
             return fail(m->ctx, JANUS_E_INVALID_ARG, "model: missing tensor in block " + std::to_string(l));
     }
+    if (int e = ensure_fused(m)) return e;   // the fused single-sequence step, either activation dtype
     if (m->cfg.act_dtype != JANUS_DT_F16) return JANUS_OK;
-    if (int e = ensure_fused(m)) return e;
     if (m->cfg.max_batch > 1 && !m->tiles_ready) {
         // tile copies for the batched MFMA products, built before any graph
         // capture: the fused QKV and gate/up weights where the fused batched

@@ -204,28 +204,29 @@ def test_dims_must_match_weight(engine):
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8, 12, 13, 1])
-@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
-def test_gemv_error_is_unbiased_across_rows(engine, ggml_type, xdt):
+@pytest.mark.parametrize("xdt,m", [(torch.float16, 1), (torch.float32, 1), (torch.float16, 8)])
+def test_gemv_error_is_unbiased_across_rows(engine, ggml_type, xdt, m):
     """The products' rounding errors are independent across rows, as the
     reference's per-element fp32 sums are: over 4096 rows of one product the
     mean of (y - y64) / sum|w x| stays a small fraction of its spread, and the
     spread stays at fp32 rounding level. An error shared by every row (a
     biased instruction, an offset term rounded once per block and reused by
     all rows) is what amplifies through the layers; the binary16 path once
-    measured a mean of -1.8e-7 there (v_dot2_f32_f16 on subnormal operands)."""
+    measured a mean of -1.8e-7 there (v_dot2_f32_f16 on subnormal operands).
+    m = 8: the small-M MFMA product, per activation row."""
     n, k = 4096, 4096
     raw, w = _weight(engine, ggml_type, n, k, 77 + ggml_type, FTZ[ggml_type])
     wf = w.dequant().double()
     rng = np.random.default_rng(ggml_type)
     means, rmss = [], []
     for _ in range(3):
-        x = torch.from_numpy(rng.standard_normal(k).astype(np.float16).astype(np.float32)).to(DEV)
-        y = torch.empty(n, device=DEV)
-        ops.gemm_auto(engine, x.to(xdt), w, y, 1, 1, k, n)
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16).astype(np.float32)).to(DEV)
+        y = torch.empty(m, n, device=DEV)
+        ops.gemm_auto(engine, x.to(xdt), w, y, m, 1, k, n)
         xd = x.double()
-        e = (y.double() - wf @ xd) / (wf.abs() @ xd.abs())
-        means.append(float(e.mean()))
-        rmss.append(float(e.pow(2).mean().sqrt()))
+        e = (y.double() - xd @ wf.T) / (xd.abs() @ wf.abs().T)
+        means.extend(e.mean(dim=1).tolist())
+        rmss.extend(e.pow(2).mean(dim=1).sqrt().tolist())
     mean, rms = float(np.mean(np.abs(means))), float(np.mean(rmss))
     assert rms < 2e-8, (means, rmss)
     assert mean < 0.25 * rms + 1e-10, (means, rmss)
