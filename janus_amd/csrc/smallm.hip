@@ -1125,16 +1125,16 @@ __global__ __launch_bounds__(1024) void epi_resnorm_kernel(GemmPartials p, const
     float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < 16; ++w) tot += red[w];
-    // x * (1 / rms) as in the M = 1 kernels' fused norm: within one ulp of
-    // x / rms, and the value is rounded to binary16 right after
-    const float inv = 1.0f / sqrtf(tot / (float)hidden + eps);
+    // (x / rms) * gamma, the reference's formula (activations.wgsl:128), as in
+    // the M = 1 kernels' fused norm
+    const float rms = sqrtf(tot / (float)hidden + eps);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t i = 4 * (threadIdx.x + 1024u * j);
         if (i < hidden) {
             *(jf4 *)(out + (size_t)m * hidden + i) = v[j];
-            const uint32_t lo = (uint32_t)f2h_bits((v[j].x * inv) * g[j].x) | ((uint32_t)f2h_bits((v[j].y * inv) * g[j].y) << 16);
-            const uint32_t hi = (uint32_t)f2h_bits((v[j].z * inv) * g[j].z) | ((uint32_t)f2h_bits((v[j].w * inv) * g[j].w) << 16);
+            const uint32_t lo = (uint32_t)f2h_bits((v[j].x / rms) * g[j].x) | ((uint32_t)f2h_bits((v[j].y / rms) * g[j].y) << 16);
+            const uint32_t hi = (uint32_t)f2h_bits((v[j].z / rms) * g[j].z) | ((uint32_t)f2h_bits((v[j].w / rms) * g[j].w) << 16);
             *(uint2 *)((uint16_t *)xn + (size_t)m * hidden + i) = make_uint2(lo, hi);
         }
     }
