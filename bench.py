@@ -125,6 +125,23 @@ def decode_bs1(engine, spec, steps: int, warmup: int, prompt_len: int = 128, pen
     return ms, toks
 
 
+def decode_stream(engine, spec, tokens: int = 96, prompt_len: int = 128):
+    """Streaming greedy decode (janus_model_generate_stream, the reference's
+    generate_with_callback) with the reference's default sampler: the median
+    interval between consecutive callbacks, in ms, over `tokens` tokens after
+    one untimed call that captures the step."""
+    from janus_amd import _lib
+    from janus_amd.model import Model
+    m = Model(engine, spec, max_seq_len=prompt_len + tokens + 8, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    prompt = np.random.default_rng(6).integers(0, spec.vocab, prompt_len).tolist()
+    m.generate_with_callback(prompt, 4, lambda t: True)
+    stamps = []
+    out = m.generate_with_callback(prompt, tokens, lambda t: stamps.append(time.perf_counter()) or True)
+    m.close()
+    gaps = np.diff(np.asarray(stamps)) * 1e3
+    return (float(np.median(gaps)) if gaps.size else float("nan")), len(out)
+
+
 L2 = dict(hidden=4096, heads=32, kv_heads=32, ffn=11008, vocab=32000, layers=32, rope_theta=10000.0)
 
 
@@ -386,7 +403,7 @@ def main() -> int:
     ap.add_argument("--no-bs32", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs1pen", "bs1ref", "bs32", "copy", "attn", "c3", "gemm",
+    ap.add_argument("--only", choices=["all", "roofline", "bs1", "bs1pen", "bs1ref", "stream", "bs32", "copy", "attn", "c3", "gemm",
                                        "kquant"],
                     default="all",
                     help="run one section alone (for rocprofv3 runs); 'all' prints the JSON line")
@@ -486,6 +503,10 @@ def main() -> int:
         msr, _ = decode_bs1(engine, spec, nref, args.warmup, f32=True)
         log(f"bs=1 reference dtypes: {msr / nref:.3f} ms/token")
         return 0
+    if args.only == "stream":
+        mss, nst = decode_stream(engine, spec)
+        log(f"bs=1 streaming: {mss:.3f} ms/token (median callback interval over {nst} tokens)")
+        return 0
     if args.only == "bs1pen":
         msp, _ = decode_bs1(engine, spec, args.steps, args.warmup, penalty=1.15, trials=HEADLINE_TRIALS)
         log(f"bs=1 penalty 1.15: {msp / args.steps:.3f} ms/token")
@@ -507,6 +528,11 @@ def main() -> int:
     bs1_ref = {"tok_s": round(nref / (msr / 1e3), 2), "ms_per_token": round(msr / nref, 4),
                "dtypes": "f32 activations into the products, f32 KV (the reference's), plain argmax"}
     log(f"bs=1 reference dtypes: {msr / nref:.3f} ms/token, {bs1_ref['tok_s']} tok/s")
+    mss, nst = decode_stream(engine, spec)
+    bs1_stream = {"ms_per_token": round(mss, 4), "tok_s": round(1e3 / mss, 2), "tokens": nst,
+                  "how": "janus_model_generate_stream with penalty 1.15: median interval between consecutive "
+                         "per-token callbacks (host wall clock)"}
+    log(f"bs=1 streaming: {mss:.3f} ms/token over {nst} tokens")
 
     bs32 = None
     if not args.no_bs32:
@@ -547,6 +573,7 @@ def main() -> int:
         "bs32": bs32,
         "bs1_penalty": bs1_pen,
         "bs1_reference_dtype": bs1_ref,
+        "bs1_stream": bs1_stream,
         "in_step": in_step,
         "gemm_m32_q4_0": gemm,
         "kquant": kq,

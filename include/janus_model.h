@@ -88,6 +88,26 @@ int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq);
  * (sampler.rs:191-193); the GPU-argmax rule ignores NaN as argmax.wgsl does. */
 int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
                          float repetition_penalty, uint32_t *out_tokens, uint32_t *n_out);
+/* Per-token callback of janus_model_generate_stream: `token` is the
+ * index-th generated token (0-based). Return nonzero to go on, 0 to stop
+ * with this token kept. It must not call into the same model. */
+typedef int (*janus_token_callback)(void *user, uint32_t token, uint32_t index);
+/* Model::generate_with_callback (generation.rs:340-604) at the token level:
+ * janus_model_generate's prefill, sampler and stop rules, with every
+ * generated token handed to cb once its step has run, in order, while the
+ * next step runs on the GPU. cb returning 0 ends generation after that token,
+ * which stays in the output (the reference pushes a token before its
+ * callback and stops when the callback returns false, generation.rs:481-509);
+ * a stop token 128001/128009 is neither returned nor passed to cb
+ * (:462-479). Text-level work (detokenising, stop strings, the UTF-8 stream
+ * decoder) belongs to the caller's callback, since token ids cross this
+ * boundary. The step queued behind the one whose token ended generation
+ * still runs (it writes one more position's K/V rows of this sequence) and
+ * its token is dropped. cb may be NULL. Tokens land in out_tokens[0, *n_out) as in
+ * janus_model_generate; the same NaN rule applies. */
+int janus_model_generate_stream(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
+                                float repetition_penalty, janus_token_callback cb, void *user, uint32_t *out_tokens,
+                                uint32_t *n_out);
 /* Model::generate_batch (generation.rs:673-870) with continuous batching:
  * request i is prompt_lens[i] token ids, the prompts back to back in
  * `prompts`. Up to max_batch requests run at once, each in its own KV slot

@@ -62,6 +62,9 @@ class ModelConfig(C.Structure):
     ]
 
 
+# janus_token_callback (include/janus_model.h); TOKEN_CALLBACK() is NULL
+TOKEN_CALLBACK = C.CFUNCTYPE(I32, P, U32, U32)
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     # context / buffers
@@ -114,6 +117,7 @@ _SIGNATURES = {
     "janus_model_kv_cache": (P, [P, I32]),
     "janus_model_read_logits": (I32, [P, P, U32]),
     "janus_model_generate": (I32, [P, P, U32, U32, F32, P, P]),
+    "janus_model_generate_stream": (I32, [P, P, U32, U32, F32, TOKEN_CALLBACK, P, P, P]),
     "janus_model_generate_batch": (I32, [P, P, P, U32, U32, F32, P, P]),
     "janus_model_set_sampler": (I32, [P, I32, F32]),
     "janus_model_graph_begin": (I32, [P, P, P, U32]),

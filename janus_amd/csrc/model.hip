@@ -77,6 +77,7 @@ struct janus_model {
     float *rope = nullptr;
     // device decode state, max_batch rows
     int32_t *d_pos = nullptr, *d_lens = nullptr, *d_tokens = nullptr, *d_rowbase = nullptr;
+    int32_t *d_feed = nullptr;   // the token each row consumes in the next step
     RowDev *d_rows = nullptr;
     int32_t *d_prompts = nullptr;   // [max_batch][max_seq_len]
     int32_t *d_out = nullptr;       // [max_batch][max_seq_len]
@@ -89,6 +90,13 @@ struct janus_model {
     std::vector<uint32_t> h_pos;   // graph_run: host mirror of the rows' positions
     uint32_t graph_nseq = 0;
     hipStream_t cap_stream = nullptr;
+    // generate_stream: pinned slots the steps' outcomes are copied to, and
+    // the events that mark them written
+    struct StreamSlot {
+        RowDev row;
+        int32_t token;
+    } *h_stream = nullptr;
+    hipEvent_t stream_ev[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -105,7 +113,7 @@ int parse_layer_name(const std::string &name, uint32_t *layer, std::string *rest
 }
 
 struct AdvanceArgs {
-    int32_t *pos, *lens, *tokens;
+    int32_t *pos, *lens, *tokens, *feed;
     RowDev *rows;
     const int32_t *prompts;
     int32_t *out;
@@ -120,8 +128,11 @@ struct AdvanceArgs {
 // lasts, the last prompt token again right after it (the first decode step
 // re-feeds it at position n, generation.rs:176,217), and from then on the
 // greedy choice of this step (best[r]). A chosen token is appended to the
-// row's generated list and counted for the repetition penalty. Done rows
-// keep their state; their attention length drops to one row.
+// row's generated list and counted for the repetition penalty. tokens[r] is
+// the last token chosen (or the next prompt token); feed[r] the token the
+// next step consumes. A row that is done keeps its feed token, position and
+// length, so a later replay recomputes its last step exactly and rewrites
+// that position's K/V rows with the values they hold.
 __global__ void advance_kernel(AdvanceArgs a) {
     const uint32_t r = threadIdx.x;
     if (r >= a.n) return;
@@ -157,9 +168,9 @@ __global__ void advance_kernel(AdvanceArgs a) {
         } else {
             a.pos[r] = p + 1;
             a.lens[r] = p + 2;
+            a.feed[r] = next;
         }
     }
-    if (c.done) a.lens[r] = 1;
     a.rows[r] = c;
 }
 
@@ -381,13 +392,14 @@ int forward_any(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uin
 int step_launch(janus_model *m, uint32_t nseq) {
     janus_ctx *ctx = m->ctx;
     const bool fold = use_fused1(m, nseq) && can_fold_head(m);
-    int e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, fold);
+    int e = forward_any(m, nullptr, m->d_feed, nseq, m->cfg.max_seq_len, fold);
     if (!e && !fold) e = argmax_keys_launch(ctx, m->logits, m->d_best, m->cfg.vocab, nseq, m->d_counts, m->d_sampler);
     if (e) return e;
     AdvanceArgs a;
     a.pos = m->d_pos;
     a.lens = m->d_lens;
     a.tokens = m->d_tokens;
+    a.feed = m->d_feed;
     a.rows = m->d_rows;
     a.prompts = m->d_prompts;
     a.out = m->d_out;
@@ -411,11 +423,12 @@ struct RowInit {
 
 // Sets the device state of the masked rows from kernel arguments, ordered on
 // the stream behind any step still reading the old values.
-__global__ void set_rows_kernel(RowInit in, int32_t *tokens, int32_t *pos, int32_t *lens, int32_t *rowbase,
-                                RowDev *rows) {
+__global__ void set_rows_kernel(RowInit in, int32_t *tokens, int32_t *feed, int32_t *pos, int32_t *lens,
+                                int32_t *rowbase, RowDev *rows) {
     const uint32_t r = threadIdx.x;
     if (r >= kMaxRows || !((in.mask[r / 32] >> (r % 32)) & 1u)) return;
     tokens[r] = in.token[r];
+    feed[r] = in.token[r];
     pos[r] = in.pos[r];
     lens[r] = in.pos[r] + 1;
     rowbase[r] = in.rowbase[r];
@@ -423,7 +436,7 @@ __global__ void set_rows_kernel(RowInit in, int32_t *tokens, int32_t *pos, int32
 }
 
 int set_rows(janus_model *m, const RowInit &in) {
-    hipLaunchKernelGGL(set_rows_kernel, dim3(1), dim3(kMaxRows), 0, m->ctx->stream, in, m->d_tokens, m->d_pos,
+    hipLaunchKernelGGL(set_rows_kernel, dim3(1), dim3(kMaxRows), 0, m->ctx->stream, in, m->d_tokens, m->d_feed, m->d_pos,
                        m->d_lens, m->d_rowbase, m->d_rows);
     JANUS_LAUNCH_CHECK(m->ctx);
     return JANUS_OK;
@@ -479,7 +492,7 @@ void free_graphs(janus_model *m) {
 int ensure_graph(janus_model *m, uint32_t nseq) {
     if (m->graphs[nseq]) return JANUS_OK;
     janus_ctx *ctx = m->ctx;
-    if (int e = forward_any(m, nullptr, m->d_tokens, nseq, m->cfg.max_seq_len, false)) return e;
+    if (int e = forward_any(m, nullptr, m->d_feed, nseq, m->cfg.max_seq_len, false)) return e;
     JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
     // Capture on the model's own stream (the caller's may be the legacy
     // default stream, which cannot be captured); the graph is launched on the
@@ -526,6 +539,38 @@ struct Request {
     uint32_t n;
 };
 
+// The prompt checks of Model::generate (generation.rs:146-150; positions 0..n-1, :161-173).
+int check_request(janus_model *m, const Request &q) {
+    const janus_model_config &c = m->cfg;
+    if (q.n == 0) return fail(m->ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
+    if (q.n > c.max_seq_len)
+        return fail(m->ctx, JANUS_E_KV_OVERFLOW, "prompt of " + std::to_string(q.n) +
+                                                     " tokens exceeds max_seq_len " + std::to_string(c.max_seq_len));
+    for (uint32_t t = 0; t < q.n; ++t)
+        if (q.prompt[t] >= c.vocab)
+            return fail(m->ctx, JANUS_E_TOKEN_RANGE, "Token ID " + std::to_string(q.prompt[t]) + " exceeds vocab size");
+    return JANUS_OK;
+}
+
+// Puts request q into row r of `in`: its prompt copied to the device, its
+// occurrence counts cleared, its first prompt token at position 0 of KV slot r.
+int admit_row(janus_model *m, uint32_t r, const Request &q, uint32_t max_tokens, int eos_mode, RowInit &in,
+              std::vector<int32_t> &tmp) {
+    janus_ctx *ctx = m->ctx;
+    const janus_model_config &c = m->cfg;
+    tmp.assign(q.prompt, q.prompt + q.n);
+    JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_prompts + (size_t)r * c.max_seq_len, tmp.data(), q.n * 4,
+                                        hipMemcpyHostToDevice, ctx->stream));
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));   // tmp is reused
+    JANUS_HIP_CHECK(ctx, hipMemsetAsync(m->d_counts + (size_t)r * c.vocab, 0, (size_t)c.vocab * 4, ctx->stream));
+    in.token[r] = (int32_t)q.prompt[0];
+    in.pos[r] = 0;
+    in.rowbase[r] = (int32_t)(r * c.max_seq_len);
+    in.ctl[r] = RowDev{(int32_t)q.n, (int32_t)max_tokens, 0, 0, eos_mode, 0};
+    in.mask[r / 32] |= 1u << (r % 32);
+    return JANUS_OK;
+}
+
 // The device-side generation loop for a list of requests, at most max_batch
 // at a time: a request takes the lowest free row (its KV slot), prefills and
 // decodes on graph replays in chunks, and frees the row when done; the next
@@ -537,19 +582,13 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
     const uint32_t B = c.max_batch;
     for (size_t i = 0; i < reqs.size(); ++i) {
         n_out[i] = 0;
-        if (reqs[i].n == 0) return fail(ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
-        if (reqs[i].n > c.max_seq_len)
-            return fail(ctx, JANUS_E_KV_OVERFLOW, "prompt of " + std::to_string(reqs[i].n) +
-                                                      " tokens exceeds max_seq_len " + std::to_string(c.max_seq_len));
-        for (uint32_t t = 0; t < reqs[i].n; ++t)
-            if (reqs[i].prompt[t] >= c.vocab)
-                return fail(ctx, JANUS_E_TOKEN_RANGE,
-                            "Token ID " + std::to_string(reqs[i].prompt[t]) + " exceeds vocab size");
+        if (int e = check_request(m, reqs[i])) return e;
     }
     if (int e = janus_model_validate(m)) return e;
     if (int e = upload_sampler(m)) return e;
     m->graph_nseq = 0;   // the rows are about to hold this loop's state, not a graph_begin's
     std::vector<int> row_req(B, -1);
+    std::vector<uint8_t> parked(B, 0);
     std::vector<RowDev> hrows(B);
     std::vector<int32_t> hpos(B, 0);
     std::vector<int32_t> tmp;
@@ -562,29 +601,32 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
         bool any_new = false;
         for (uint32_t r = 0; r < B && next_req < reqs.size(); ++r) {
             if (row_req[r] >= 0) continue;
-            const Request &q = reqs[next_req];
-            row_req[r] = (int)next_req++;
-            tmp.assign(q.prompt, q.prompt + q.n);
-            JANUS_HIP_CHECK(ctx, hipMemcpyAsync(m->d_prompts + (size_t)r * c.max_seq_len, tmp.data(), q.n * 4,
-                                                hipMemcpyHostToDevice, ctx->stream));
-            JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));   // tmp is reused
-            JANUS_HIP_CHECK(ctx, hipMemsetAsync(m->d_counts + (size_t)r * c.vocab, 0, (size_t)c.vocab * 4, ctx->stream));
-            in.token[r] = (int32_t)q.prompt[0];
-            in.pos[r] = 0;
-            in.rowbase[r] = (int32_t)(r * c.max_seq_len);
-            in.ctl[r] = RowDev{(int32_t)q.n, (int32_t)max_tokens, 0, 0, eos_mode, 0};
-            in.mask[r / 32] |= 1u << (r % 32);
+            row_req[r] = (int)next_req;
+            parked[r] = 0;
+            if (int e = admit_row(m, r, reqs[next_req++], max_tokens, eos_mode, in, tmp)) return e;
             hrows[r] = in.ctl[r];
             hpos[r] = 0;
             any_new = true;
         }
-        if (any_new)
-            if (int e = set_rows(m, in)) return e;
         uint32_t nrows = 0;
         for (uint32_t r = 0; r < B; ++r)
             if (row_req[r] >= 0) nrows = r + 1;
         if (nrows == 0) break;
-        // free rows below nrows stay done (frozen) until a request takes them
+        // A free row below nrows still runs through every replay: park it at
+        // position 0 of its own (free) slot with one row of attention, so it
+        // costs little until a request takes it.
+        for (uint32_t r = 0; r < nrows; ++r) {
+            if (row_req[r] >= 0 || parked[r]) continue;
+            in.token[r] = 0;
+            in.pos[r] = 0;
+            in.rowbase[r] = (int32_t)(r * c.max_seq_len);
+            in.ctl[r] = RowDev{0, 0, 0, 1, EOS_IGNORE, 0};
+            in.mask[r / 32] |= 1u << (r % 32);
+            parked[r] = 1;
+            any_new = true;
+        }
+        if (any_new)
+            if (int e = set_rows(m, in)) return e;
         if (int e = ensure_graph(m, nrows)) return e;
         // steps until the first row can be done without an EOS: its prompt,
         // its tokens, or its capacity
@@ -622,6 +664,76 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
     return JANUS_OK;
 }
 
+// The streaming form of run_requests for one request in row 0: the prompt
+// on replays of the captured step, then one replay per token with the row's
+// control block and its token copied behind it to pinned host memory; the
+// host hands step i's token to the callback while step i + 1 runs.
+int run_stream(janus_model *m, const Request &q, uint32_t max_tokens, janus_token_callback cb, void *user,
+               uint32_t *out_tokens, uint32_t *n_out) {
+    janus_ctx *ctx = m->ctx;
+    if (int e = check_request(m, q)) return e;
+    if (int e = janus_model_validate(m)) return e;
+    if (int e = upload_sampler(m)) return e;
+    if (!m->h_stream) {
+        void *h = nullptr;
+        JANUS_HIP_CHECK(ctx, hipHostMalloc(&h, 2 * sizeof(janus_model::StreamSlot), hipHostMallocDefault));
+        m->h_stream = (janus_model::StreamSlot *)h;
+    }
+    for (hipEvent_t &ev : m->stream_ev)
+        if (!ev) JANUS_HIP_CHECK(ctx, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    m->graph_nseq = 0;   // row 0 is about to hold this loop's state, not a graph_begin's
+    RowInit in;
+    std::memset(&in, 0, sizeof(in));
+    in.set_ctl = 1;
+    std::vector<int32_t> tmp;
+    if (int e = admit_row(m, 0, q, max_tokens, EOS_STOP_DROP, in, tmp)) return e;
+    if (int e = set_rows(m, in)) return e;
+    if (int e = ensure_graph(m, 1)) return e;
+    // prefill: positions 0 .. n-1; the last of these steps queues the re-fed
+    // last prompt token at position n (or ends the row at max_seq_len)
+    if (int e = replay(m, 1, q.n)) return e;
+    // step i samples token i; at most max_tokens steps can sample one
+    auto issue = [&](uint32_t i) -> int {
+        janus_model::StreamSlot *slot = m->h_stream + (i & 1);
+        if (int e = replay(m, 1, 1)) return e;
+        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&slot->row, m->d_rows, sizeof(RowDev), hipMemcpyDeviceToHost, ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&slot->token, m->d_tokens, 4, hipMemcpyDeviceToHost, ctx->stream));
+        JANUS_HIP_CHECK(ctx, hipEventRecord(m->stream_ev[i & 1], ctx->stream));
+        return JANUS_OK;
+    };
+    uint32_t n = 0;
+    int status = JANUS_OK;
+    if (int e = issue(0)) return e;
+    for (uint32_t i = 0;; ++i) {
+        // queue step i + 1 before waiting for step i (its slot was read in
+        // iteration i - 1)
+        if (i + 1 < max_tokens)
+            if ((status = issue(i + 1))) break;
+        hipError_t we = hipEventSynchronize(m->stream_ev[i & 1]);
+        if (we != hipSuccess) {
+            status = hip_fail(ctx, we, "hipEventSynchronize");
+            break;
+        }
+        const janus_model::StreamSlot got = m->h_stream[i & 1];
+        if (got.row.nan) {
+            status = nan_fail(ctx, 0);
+            break;
+        }
+        bool stop = got.row.done || i + 1 >= max_tokens;
+        if ((uint32_t)got.row.nout > n) {   // this step pushed a token (a stop token is not pushed)
+            out_tokens[n] = (uint32_t)got.token;
+            ++n;
+            if (cb && !cb(user, (uint32_t)got.token, n - 1)) stop = true;
+        }
+        if (stop) break;
+    }
+    *n_out = n;
+    // the step queued behind the last one read still runs; leave the stream idle
+    const hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (status == JANUS_OK && se != hipSuccess) status = hip_fail(ctx, se, "hipStreamSynchronize");
+    return status;
+}
+
 }  // namespace
 
 extern "C" {
@@ -656,6 +768,7 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
               alloc(&m->act, B * c.ffn * 4) && alloc(&m->attn16, B * c.hidden * 2) &&
               alloc((void **)&m->rope, S * c.head_dim * 4) && alloc((void **)&m->d_pos, kMaxRows * 4) &&
               alloc((void **)&m->d_lens, kMaxRows * 4) && alloc((void **)&m->d_tokens, kMaxRows * 4) &&
+              alloc((void **)&m->d_feed, kMaxRows * 4) &&
               alloc((void **)&m->d_rowbase, kMaxRows * 4) && alloc((void **)&m->d_rows, kMaxRows * sizeof(RowDev)) &&
               alloc((void **)&m->d_prompts, B * S * 4) && alloc((void **)&m->d_out, B * S * 4) &&
               alloc((void **)&m->d_counts, B * c.vocab * 4) && alloc((void **)&m->d_best, kMaxRows * 8) &&
@@ -664,6 +777,7 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
          hipMemset(m->d_rows, 0, kMaxRows * sizeof(RowDev)) == hipSuccess &&
          hipMemset(m->d_counts, 0, B * c.vocab * 4) == hipSuccess &&
          hipMemset(m->d_pos, 0, kMaxRows * 4) == hipSuccess && hipMemset(m->d_tokens, 0, kMaxRows * 4) == hipSuccess &&
+         hipMemset(m->d_feed, 0, kMaxRows * 4) == hipSuccess &&
          hipMemcpy(m->d_sampler, &m->h_sampler, sizeof(SamplerDev), hipMemcpyHostToDevice) == hipSuccess;
     if (ok) {
         std::vector<int32_t> base(kMaxRows, 0), ones(kMaxRows, 1);
@@ -704,6 +818,9 @@ void janus_model_destroy(janus_model *m) {
     hipStreamSynchronize(m->ctx->stream);
     free_graphs(m);
     if (m->cap_stream) hipStreamDestroy(m->cap_stream);
+    for (hipEvent_t ev : m->stream_ev)
+        if (ev) hipEventDestroy(ev);
+    if (m->h_stream) hipHostFree(m->h_stream);
     for (auto &L : m->layers) {
         for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down, L.qkv, L.gu}) janus_weight_free(m->ctx, w);
         hipFree(L.attn_norm);
@@ -714,7 +831,7 @@ void janus_model_destroy(janus_model *m) {
     for (void *p : {(void *)m->out_norm, (void *)m->hidden, (void *)m->q, (void *)m->k, (void *)m->v,
                     (void *)m->attn, m->attn16, (void *)m->h1, (void *)m->gate, (void *)m->up, (void *)m->logits, m->xn,
                     m->act, m->kv_external ? nullptr : m->kcache, m->kv_external ? nullptr : m->vcache,
-                    (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens, (void *)m->d_tokens, (void *)m->d_rowbase,
+                    (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens, (void *)m->d_tokens, (void *)m->d_feed, (void *)m->d_rowbase,
                     (void *)m->d_rows, (void *)m->d_prompts, (void *)m->d_out, (void *)m->d_counts,
                     (void *)m->d_best, (void *)m->d_sampler})
         if (p) hipFree(p);
@@ -905,6 +1022,21 @@ int janus_model_generate(janus_model *m, const uint32_t *prompt, uint32_t n_prom
     }
     std::vector<Request> reqs{Request{prompt, n_prompt}};
     return run_requests(m, reqs, max_tokens, EOS_STOP_DROP, out_tokens, n_out);
+}
+
+int janus_model_generate_stream(janus_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_tokens,
+                                float penalty, janus_token_callback cb, void *user, uint32_t *out_tokens,
+                                uint32_t *n_out) {
+    if (!m || !prompt || !out_tokens || !n_out) return JANUS_E_INVALID_ARG;
+    *n_out = 0;
+    if (n_prompt == 0) return fail(m->ctx, JANUS_E_INVALID_ARG, "Empty prompt after tokenization");
+    if (!(penalty > 0.0f) || !std::isfinite(penalty))
+        return fail(m->ctx, JANUS_E_INVALID_ARG, "generate_stream: penalty must be positive and finite");
+    // the same sampler as generate (Sampler::sample, sampler.rs:154-160, 188-206)
+    m->h_sampler.mode = std::fabs(penalty - 1.0f) < 0.01f ? SAMPLE_WGSL : SAMPLE_PENALTY;
+    m->h_sampler.penalty = penalty;
+    if (max_tokens == 0) return janus_model_generate(m, prompt, n_prompt, 0, penalty, out_tokens, n_out);
+    return run_stream(m, Request{prompt, n_prompt}, max_tokens, cb, user, out_tokens, n_out);
 }
 
 int janus_model_generate_batch(janus_model *m, const uint32_t *prompts, const uint32_t *prompt_lens, uint32_t nreq,

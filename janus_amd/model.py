@@ -8,7 +8,7 @@ loop and greedy-sampler semantics (generation.rs:129-323).
 from __future__ import annotations
 
 import ctypes as C
-from typing import Sequence
+from typing import Callable, Sequence
 
 import numpy as np
 
@@ -102,6 +102,33 @@ class Model:
         n = C.c_uint32()
         self._check(self.lib.janus_model_generate(self.handle, p.ctypes.data, len(p), max_tokens,
                                                   repetition_penalty, out.ctypes.data, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def generate_with_callback(self, prompt: Sequence[int], max_tokens: int,
+                               callback: Callable[[int], bool] | None = None,
+                               repetition_penalty: float = 1.15) -> list[int]:
+        """Model::generate_with_callback (generation.rs:340-604) on token ids:
+        `callback(token)` runs for each generated token as its step finishes
+        and stops generation, with that token kept, by returning False. An
+        exception raised by the callback stops generation and is re-raised."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint32))
+        out = np.zeros(max(1, max_tokens), dtype=np.uint32)
+        n = C.c_uint32()
+        raised: list[BaseException] = []
+
+        def trampoline(_user, token, _index):
+            try:
+                return 1 if callback(int(token)) else 0
+            except BaseException as exc:   # never unwind through the C frames
+                raised.append(exc)
+                return 0
+
+        cb = _lib.TOKEN_CALLBACK(trampoline) if callback is not None else _lib.TOKEN_CALLBACK()
+        status = self.lib.janus_model_generate_stream(self.handle, p.ctypes.data, len(p), max_tokens,
+                                                      repetition_penalty, cb, None, out.ctypes.data, C.byref(n))
+        if raised:
+            raise raised[0]
+        self._check(status)
         return out[: n.value].tolist()
 
     def generate_batch(self, prompts: Sequence[Sequence[int]], max_tokens: int,

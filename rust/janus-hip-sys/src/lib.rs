@@ -22,6 +22,9 @@ pub struct janus_weight {
 pub struct janus_model {
     _p: [u8; 0],
 }
+/// Per-token callback of `janus_model_generate_stream` (`None` is NULL):
+/// nonzero to go on, 0 to stop with this token kept.
+pub type janus_token_callback = Option<unsafe extern "C" fn(user: *mut c_void, token: u32, index: u32) -> c_int>;
 
 // ---- constants (enums and #defines of the headers) ----
 pub const JANUS_OK: c_int = 0;
@@ -322,6 +325,17 @@ unsafe extern "C" {
         n_prompt: u32,
         max_tokens: u32,
         repetition_penalty: c_float,
+        out_tokens: *mut u32,
+        n_out: *mut u32,
+    ) -> c_int;
+    pub fn janus_model_generate_stream(
+        m: *mut janus_model,
+        prompt: *const u32,
+        n_prompt: u32,
+        max_tokens: u32,
+        repetition_penalty: c_float,
+        cb: janus_token_callback,
+        user: *mut c_void,
         out_tokens: *mut u32,
         n_out: *mut u32,
     ) -> c_int;

@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+import decode_models as DM
 from greedy import assert_same_or_near_tie
 from janus_amd import _lib, ops, synth
 from janus_amd.model import Model
@@ -26,8 +27,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _prompt(seed, n, vocab):
-    return np.random.default_rng(seed).integers(0, vocab, n).tolist()
+_prompt = DM.prompt
 
 
 def _rel_err(a, b):
@@ -239,41 +239,9 @@ def test_generate_batch_capacity_and_empty_prompt(engine, spec):
     m.close()
 
 
-def _eos_spec():
-    """Vocabulary of 128256 with an LM head that is zero except row 128009, set
-    to the sign pattern of the first decode step's normalised hidden state of
-    prompt A: A's first sampled token is the stop token 128009; for other
-    prompts the oracle decides."""
-    s = synth.make_model(83, 256, 4, 2, 512, 128256, 1, synth.Q8_0, 1e-5, 10000.0,
-                         embed_type=synth.F16, head_type=synth.F16)
-    return s
-
-
 def test_stop_token_generate_drops_batch_keeps(engine):
-    s = _eos_spec()
     pa = [11, 22, 33]
-    ref = O.OracleModel(s, 16)
-    for p, t in enumerate(pa):
-        ref.forward(t, p)
-    # the normalised hidden of the decode step at position 3 (token 33)
-    xs = {}
-    orig = O.rmsnorm
-
-    def spy(x, gamma, eps):
-        xs["last"] = np.array(x, copy=True)
-        return orig(x, gamma, eps)
-
-    O.rmsnorm = spy
-    try:
-        ref.forward(33, 3)
-    finally:
-        O.rmsnorm = orig
-    xn = O.rmsnorm(xs["last"], [t for t in s.tensors if t.name == "output_norm.weight"][0].data, s.rms_eps)
-    head = np.zeros((s.vocab, s.hidden), np.float32)
-    head[128009] = np.sign(xn) * np.float32(0.05)
-    head[77] = np.sign(xn) * np.float32(0.01)
-    s.tensors = [t for t in s.tensors if t.name != "output.weight"]
-    s.tensors.append(synth.Tensor("output.weight", synth.F16, s.vocab, s.hidden, synth.f16_bits(head)))
+    s = DM.eos_model(pa)
     want_single = O.OracleModel(s, 16).generate(pa, 5, 1.15)
     want_batch = O.OracleModel(s, 16).generate(pa, 5, 1.15, batch_rules=True)
     assert want_single == [] and want_batch == [128009]
@@ -325,19 +293,6 @@ def test_workspace_growth_keeps_captured_step():
     engine.close()
 
 
-def _nan_head_spec():
-    """A one-layer model whose F16 LM head holds a NaN in row 321, so every
-    step's logit 321 is NaN."""
-    s = synth.make_model(97, 256, 4, 2, 512, 1000, 1, synth.Q8_0, 1e-5, 10000.0,
-                         embed_type=synth.F16, head_type=synth.F16)
-    head = [t for t in s.tensors if t.name == "output.weight"][0]
-    bits = np.array(head.data, dtype=np.uint16, copy=True).reshape(s.vocab, s.hidden)
-    bits[321, 17] = 0x7E00
-    s.tensors = [t for t in s.tensors if t.name != "output.weight"]
-    s.tensors.append(synth.Tensor("output.weight", synth.F16, s.vocab, s.hidden, bits.reshape(-1)))
-    return s
-
-
 def test_nan_logits_refused_under_cpu_sampler_rules(engine):
     """NaN logits: the reference's CPU sampler (penalty != 1, and every batch)
     panics (sampler.rs:191-193, 397-399), so generate, generate_batch and a
@@ -345,7 +300,7 @@ def test_nan_logits_refused_under_cpu_sampler_rules(engine):
     JANUS_E_NAN_LOGITS, and no token is chosen at that step. The GPU-argmax
     rule (|penalty - 1| < 0.01) ignores NaN as argmax.wgsl does and follows
     the oracle."""
-    s = _nan_head_spec()
+    s = DM.nan_head_model()
     prompt = _prompt(98, 5, s.vocab)
     m = Model(engine, s, max_seq_len=32, max_batch=2)
     m.forward([prompt[0]], [0])

@@ -102,3 +102,16 @@ def test_model_config_layout_matches_the_header():
     assert len(cfields) == 13
     assert rfields == cfields
     assert "#[repr(C)]\n#[derive(Clone, Copy, Debug, Default)]\npub struct janus_model_config" in rs
+
+
+def test_token_callback_type_matches_the_header():
+    """janus_token_callback crosses the boundary as a nullable function
+    pointer with the header's parameter and return types."""
+    h = (ROOT / "include" / "janus_model.h").read_text()
+    m = re.search(r"typedef (\w+) \(\*janus_token_callback\)\((.*?)\);", h, re.S)
+    cargs = [_c_to_rust(re.match(r"(.*?)(\w+)$", p.strip()).group(1)) for p in m.group(2).split(",")]
+    r = re.search(r"pub type janus_token_callback = Option<unsafe extern \"C\" fn\((.*?)\) -> (\w+)>;",
+                  LIB_RS.read_text())
+    rargs = [" ".join(p.split(":", 1)[1].split()) for p in r.group(1).split(",")]
+    assert rargs == cargs
+    assert r.group(2) == _c_to_rust(m.group(1))
