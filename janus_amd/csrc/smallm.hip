@@ -133,15 +133,52 @@ struct GemmArgs {
 // W: one chunk of one lane. load() reads it; mma() adds its contribution for
 // MT M-tiles given the LDS A slice (row stride pitch) at chunk offset kl.
 
+// Block results whose scale is applied one block later: the scale FMAs of a
+// block then run while the next block's MFMAs are in flight instead of
+// waiting for their own (the same FMAs in the same order).
+template <int MT> struct Deferred {
+    f16x t[MT];   // the last block's MFMA results
+    float d;      // and its scale (0 before the first block)
+};
+
 struct GQ4_0 {
     static constexpr int CK = 64;
+    static constexpr bool DEFER = true;
     struct W { uint4 q; uint32_t s; };
+    // g and c are wavefront-uniform: the chunk base is scalar, the lane adds
+    // a 32-bit offset
     __device__ static W load(const GemmArgs &a, uint32_t g, uint32_t c, int lane) {
         const size_t ch = (size_t)g * a.chunks + c;
         W w;
-        w.q = ld_stream(a.qs + (ch * 64 + lane) * 16);
-        w.s = ((const uint32_t *)a.side)[ch * 32 + (lane & 31)];
+        w.q = ld_stream(a.qs + ch * 1024 + (uint32_t)lane * 16u);
+        w.s = *(const uint32_t *)(a.side + ch * 128 + (uint32_t)(lane & 31) * 4u);
         return w;
+    }
+    template <int MT>
+    __device__ static void mma_deferred(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
+                                        f16x (&acc)[MT], Deferred<MT> &pend) {
+        const int h = lane >> 5, r = lane & 31;
+        const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const h8 b0 = unpack_nib8(q[2 * b], (_Float16)1032.0f);
+            const h8 b1 = unpack_nib8(q[2 * b + 1], (_Float16)1032.0f);
+            const float d = h2f((uint16_t)(b ? (w.s >> 16) : (w.s & 0xffffu)));
+            f16x t[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const _Float16 *ap = As + (size_t)(mt * 32 + r) * pitch + kl + b * 32 + 8 * h;
+                t[mt] = mfma(lds_h8(ap), b0, (f16x){});
+                t[mt] = mfma(lds_h8(ap + 16), b1, t[mt]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[mt][v] = fmaf(pend.d, pend.t[mt][v], acc[mt][v]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) pend.t[mt] = t[mt];
+            pend.d = d;
+        }
     }
     template <int MT>
     __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,
@@ -303,6 +340,18 @@ struct GQ5_K {
     }
 };
 
+// formats whose block scales are applied one block late (mma_deferred)
+template <class F, class = void> struct Defers { static constexpr bool value = false; };
+template <class F> struct Defers<F, std::void_t<decltype(F::DEFER)>> { static constexpr bool value = F::DEFER; };
+
+template <int MT>
+__device__ __forceinline__ void flush_deferred(f16x (&acc)[MT], const Deferred<MT> &pend) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mt][v] = fmaf(pend.d, pend.t[mt][v], acc[mt][v]);
+}
+
 // formats whose mins need the per-(row, sub-block) activation sums in LDS
 template <class F> struct NeedsSums { static constexpr bool value = false; };
 template <> struct NeedsSums<GQ4_K> { static constexpr bool value = true; };
@@ -383,7 +432,8 @@ template <class F, int MT, int KW, int SPT, int PD = Stage<F>::PD>
 __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr bool SUMS = NeedsSums<F>::value;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar chunk bases
     const int rgw = wave % WAVES, kw = wave / WAVES;   // row group in the tile, K slice of the pass
     const uint32_t G = (a.n + 31) / 32;
     const uint32_t tile = blockIdx.x, ks = blockIdx.y;
@@ -396,6 +446,10 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
     f16x acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (f16x){};
+    Deferred<MT> pend;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pend.t[mt] = (f16x){};
+    pend.d = 0.0f;
 
     const uint32_t cpk = a.pass_chunks / KW;   // chunks per K slice
     const uint32_t p_begin = ks * a.passes_per_wg;
@@ -449,7 +503,12 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
         auto compute = [&](typename F::W (&w)[PD], uint32_t cs) {
 #pragma unroll
             for (int i = 0; i < PD; ++i)
-                if (cs + i < m1) F::template mma<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, Ss, 0, acc);
+                if (cs + i < m1) {
+                    if constexpr (Defers<F>::value)
+                        F::template mma_deferred<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, acc, pend);
+                    else
+                        F::template mma<MT>(w[i], As, a.pitch, (cs + i - c0) * F::CK, lane, Ss, 0, acc);
+                }
         };
         uint32_t cs = m0;
         for (; cs + PD < m1; cs += 2 * PD) {
@@ -460,6 +519,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
         }
         if (cs < m1) compute(wa, cs);
     }
+    if constexpr (Defers<F>::value) flush_deferred<MT>(acc, pend);
 
     // add the K slices of each row group in slice order (LDS, reusing the A area)
     if (KW > 1) {
@@ -520,7 +580,8 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) 
     static_assert(CPW >= 1 && CPW * KW == PC && SPT >= 1 && SPT * NT == MP * SEGS, "pass shape");
     constexpr uint32_t ABYTES = (uint32_t)MP * PITCH * 2;
     constexpr uint32_t BUF = (ABYTES + (SUMS ? (uint32_t)(KR / 32) * MP * 4 : 0u) + 15u) / 16u * 16u;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar chunk bases
     const int rgw = wave % WAVES, kw = wave / WAVES;
     const uint32_t G = (a.n + 31) / 32;
     const uint32_t g = blockIdx.x * WAVES + rgw, ks = blockIdx.y;
@@ -531,6 +592,10 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) 
     f16x acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (f16x){};
+    Deferred<MT> pend;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pend.t[mt] = (f16x){};
+    pend.d = 0.0f;
     typename F::W w[CPW];
     uint4 sv[SPT];
 
@@ -585,7 +650,12 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) 
         const uint32_t c1 = min(a.chunks, (p + 1) * PC), m0 = p * PC + kw * CPW;
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
-            if (m0 + i < c1) F::template mma<MT>(w[i], As, PITCH, (uint32_t)(kw * CPW + i) * F::CK, lane, Ss, 0, acc);
+            if (m0 + i < c1) {
+                if constexpr (Defers<F>::value)
+                    F::template mma_deferred<MT>(w[i], As, PITCH, (uint32_t)(kw * CPW + i) * F::CK, lane, acc, pend);
+                else
+                    F::template mma<MT>(w[i], As, PITCH, (uint32_t)(kw * CPW + i) * F::CK, lane, Ss, 0, acc);
+            }
             if (decltype(load_next)::value) w[i] = F::load(a, gl, chunk_of(p + 1, i), lane);
         }
     };
@@ -614,6 +684,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_pipe_kernel(GemmArgs a) 
         }
         pass(last, std::false_type{});
     }
+    if constexpr (Defers<F>::value) flush_deferred<MT>(acc, pend);
 
     if (KW > 1) {
         float *red = (float *)smem;
