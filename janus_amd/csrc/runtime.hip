@@ -326,7 +326,7 @@ int janus_create(int hip_device, janus_ctx **out) {
     }
     if (const char *k = std::getenv("JANUS_GEMV_LDS_THREADS")) {
         const int v = std::atoi(k);
-        if (v == 512 || v == 1024) ctx->gemv_lds_threads = (uint32_t)v;
+        if (v >= 256 && v <= 1024 && v % 64 == 0) ctx->gemv_lds_threads = (uint32_t)v;
     }
     if (const char *k = std::getenv("JANUS_GEMV_F16_ROWS")) ctx->gemv_f16_rows2 = std::strcmp(k, "1") != 0;
     if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
