@@ -411,18 +411,24 @@ struct FQ4_K {
     static constexpr int UNIT = 32;
     static constexpr bool XREREAD = true;   // long rows re-read x from LDS per row group
     static constexpr bool PERM = true;
-    // The 16-byte super-block header (d, dmin, 12 scale bytes) is shared by
-    // the 8 units of a super-block, which sit on 8 consecutive lanes in every
-    // kernel (units are lane-contiguous and a row holds a multiple of 8): each
-    // lane keeps one header word (lane & 3) and the quad rebuilds the header
-    // with DPP broadcasts at use, 1 VGPR per unit instead of 4.
+    // The 16-byte super-block header (d, dmin, the scale fields of kq_group
+    // in words 1-3) is shared by the 8 units of a super-block, which sit on 8
+    // consecutive lanes in every kernel, unit c on lane p = lane & 7 (units
+    // are lane-contiguous from a multiple of 8 and a row holds a multiple of
+    // 8). Lane p keeps header word hword(p) = {0, 1, 1, 2, 0, 2, 3, 3}[p]:
+    // quad DPP reads of lanes [0,0,0,0], [1,1,2,2] and [3,3,3,3] then hand
+    // every lane d / dmin and the words (lo, hi) = (1, 2) for chunk pairs
+    // j = 0, 1 (first quad), (2, 3) for j = 2 and (3, 3) for j = 3 (second
+    // quad), whose funnel shift by (32 - 8j) & 31 is the lane's field. One
+    // VGPR of header per unit, three DPP moves and one shift at use.
     struct W { uint4 q; uint32_t hw; };
+    __device__ static uint32_t hword() { return (0x33202110u >> (4u * (__lane_id() & 7u))) & 15u; }
     __device__ static W load(WPtr w, size_t unit) {
         size_t sb = unit >> 3;
         int c = (int)(unit & 7);
         const uint4 *blk = (const uint4 *)(w.qs + sb * 144);
         W r;
-        r.hw = ((const uint32_t *)blk)[__lane_id() & 3];
+        r.hw = ((const uint32_t *)blk)[hword()];
         r.q = ld_stream(blk + 1 + c);
         return r;
     }
@@ -431,18 +437,15 @@ struct FQ4_K {
         const uint8_t *row = w.qs + (ru >> 3) * 144;   // uniform; one 32-bit lane offset per load
         const uint32_t ob = (u >> 3) * 144u;
         W r;
-        r.hw = *(const uint32_t *)(row + (ob + 4u * (__lane_id() & 3)));
+        r.hw = *(const uint32_t *)(row + (ob + 4u * hword()));
         r.q = ld_stream(row + (ob + 16u + 16u * (u & 7u)));
         return r;
     }
-    template <int T> __device__ static uint32_t quad_word(uint32_t v) {
-        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, T * 0x55, 0xf, 0xf, false);   // quad_perm [T,T,T,T]
-    }
-    template <class WW> __device__ static uint4 header(const WW &w) {
-        return make_uint4(quad_word<0>(w.hw), quad_word<1>(w.hw), quad_word<2>(w.hw), quad_word<3>(w.hw));
+    template <int PERM> __device__ static uint32_t quad_read(uint32_t v) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, PERM, 0xf, 0xf, false);
     }
     // x for one chunk: 16 low-nibble elements and 16 high-nibble elements.
-    struct XF { jf4 lo[4], hi[4]; float slo, shi; int c; };
+    struct XF { jf4 lo[4], hi[4]; float slo, shi; };
     __device__ static XF loadx(const float *xs, const float *sx16, int u) {
         int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
         int blo = sb * 8 + 2 * j, bhi = blo + 1;   // 32-element LDS blocks
@@ -453,10 +456,9 @@ struct FQ4_K {
         for (int i = 0; i < 4; ++i) { r.lo[i] = pl[i]; r.hi[i] = ph[i]; }
         r.slo = sx16[2 * blo + h];
         r.shi = sx16[2 * bhi + h];
-        r.c = c;
         return r;
     }
-    struct XH { jh2 lo[8], hi[8]; float slo, shi; int c; };
+    struct XH { jh2 lo[8], hi[8]; float slo, shi; };
     __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) {
         int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
         int blo = sb * 8 + 2 * j, bhi = blo + 1;
@@ -473,7 +475,6 @@ struct FQ4_K {
         }
         r.slo = sx16[2 * blo + h];
         r.shi = sx16[2 * bhi + h];
-        r.c = c;
         return r;
     }
     __device__ static XF loadx_g(const float *x, int u) {
@@ -490,7 +491,6 @@ struct FQ4_K {
         }
         r.slo = sl;
         r.shi = sh;
-        r.c = c;
         return r;
     }
     __device__ static XH loadx_g(const _Float16 *x, int u) {
@@ -499,31 +499,17 @@ struct FQ4_K {
         XH r;
         r.slo = load16h_perm(base, r.lo);
         r.shi = load16h_perm(base + 32, r.hi);
-        r.c = c;
         return r;
-    }
-    // (sc, m) pair of sub-block `sub` from the 12 scale bytes held in hdr.y..w
-    // (bytes 0-3, 4-7, 8-11). `sub` differs between lanes, so both forms are
-    // computed and selected: a branch would run both under exec masks.
-    __device__ static void scale_min(const uint4 &hdr, int sub, float &sc, float &mn) {
-        const uint32_t sh = 8u * (uint32_t)(sub & 3);
-        const uint32_t b0 = hdr.y >> sh, b1 = hdr.z >> sh, b2 = hdr.w >> sh;
-        const bool low = sub < 4;
-        // sub < 4: low 6 bits of byte sub of s0 / s1; else the nibbles of byte
-        // sub - 4 of s2 with bits 6-7 of byte sub - 4 of s0 / s1 on top
-        const uint32_t scv = low ? (b0 & 63u) : ((b2 & 15u) | ((b0 >> 2) & 48u));
-        const uint32_t mnv = low ? (b1 & 63u) : (((b2 >> 4) & 15u) | ((b1 >> 2) & 48u));
-        sc = (float)scv;
-        mn = (float)mnv;
     }
     template <class WW, class X>
     __device__ static float finish(const WW &w, const X &x, float qlo, float qhi) {
-        const uint4 hdr = header(w);
-        float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
-        int j = x.c >> 1;
-        float sl, ml, sh, mh;
-        scale_min(hdr, 2 * j, sl, ml);
-        scale_min(hdr, 2 * j + 1, sh, mh);
+        const uint32_t dd = quad_read<0x00>(w.hw);   // quad_perm [0,0,0,0]
+        const uint32_t lo = quad_read<0xa5>(w.hw);   // [1,1,2,2]
+        const uint32_t hi = quad_read<0xff>(w.hw);   // [3,3,3,3]
+        const uint32_t g = __builtin_amdgcn_alignbit(hi, lo, (0u - 4u * (__lane_id() & 6u)) & 31u);
+        const float d = h2f((uint16_t)(dd & 0xffffu)), dmin = h2f((uint16_t)(dd >> 16));
+        const float sl = (float)(g & 63u), sh = (float)((g >> 6) & 63u);
+        const float ml = (float)((g >> 12) & 63u), mh = (float)((g >> 18) & 63u);
         float r = (d * sl) * qlo;
         r = fmaf(d * sh, qhi, r);
         r = fmaf(-(dmin * ml), x.slo, r);
@@ -583,7 +569,7 @@ struct FQ5_K : FQ4_K {
         const uint8_t *row = w.qs + (ru >> 3) * 176;   // uniform; one 32-bit lane offset per load
         const uint32_t ob = (u >> 3) * 176u, c = u & 7u;
         W r;
-        r.hw = *(const uint32_t *)(row + (ob + 4u * (__lane_id() & 3)));
+        r.hw = *(const uint32_t *)(row + (ob + 4u * hword()));
 #if !defined(JANUS_GEMV_NT) || JANUS_GEMV_NT
         r.qh = __builtin_nontemporal_load((const uint32_t *)(row + (ob + 16u + 4u * c)));
 #else
@@ -597,7 +583,7 @@ struct FQ5_K : FQ4_K {
         int c = (int)(unit & 7);
         const uint4 *blk = (const uint4 *)(w.qs + sb * 176);
         W r;
-        r.hw = ((const uint32_t *)blk)[__lane_id() & 3];
+        r.hw = ((const uint32_t *)blk)[hword()];
 #if !defined(JANUS_GEMV_NT) || JANUS_GEMV_NT
         r.qh = __builtin_nontemporal_load((const uint32_t *)blk + 4 + c);
 #else

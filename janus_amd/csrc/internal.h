@@ -89,9 +89,12 @@ struct SamplerDev {
 //  Q4_0 : qs  = n * nb * 16 bytes (GGML nibble order per block), 16-B aligned
 //         sc  = n * nb binary16 scales (nb = k / 32)
 //  Q8_0 : qs  = n * nb * 32 bytes (int8), sc = n * nb binary16 scales
-//  Q4_K : qs  = the GGML 144-byte super-blocks, unchanged, 256-B aligned base
-//  Q5_K : qs  = the GGML 176-byte super-blocks with qh[32] rewritten as one
-//         32-bit word of high bits per 16-byte quant chunk (q5k_pack_high_bits)
+//  Q4_K : qs  = the GGML 144-byte super-blocks, 256-B aligned base, with the
+//         12 scale bytes rewritten as chunk-pair fields (kquant_pack_scales,
+//         read by kq_group)
+//  Q5_K : qs  = the GGML 176-byte super-blocks, scale bytes as Q4_K, with
+//         qh[32] rewritten as one 32-bit word of high bits per 16-byte quant
+//         chunk (q5k_pack_high_bits)
 //  F16  : qs  = n * k binary16, row-major, FTZ applied at upload when flagged
 struct janus_weight {
     int type = 0;
@@ -281,6 +284,19 @@ __device__ __forceinline__ uint4 ld_stream(const void *p) {
 // with f16 denormals enabled (the gfx950 default for HIP).
 __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// K-quant (Q4_K / Q5_K) scales in HBM. Bytes 0-3 of a super-block are d and
+// dmin (binary16), as in GGML. The 12 bytes after them, little-endian words
+// s0, s1, s2 (96 bits), hold for chunk pair j = 0..3 (quant bytes 32j ..
+// 32j + 31, sub-blocks 2j and 2j + 1) the 24-bit field at bit 24j:
+// sc(2j), sc(2j + 1), m(2j), m(2j + 1), six bits each from the low end. GGML
+// spreads sub-blocks 4..7 over three bytes each (get_scale_min_k4); here one
+// funnel shift gives a chunk its whole field. Returns that field in bits 0-23.
+__device__ __forceinline__ uint32_t kq_group(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j) {
+    const uint32_t lo = j < 2 ? s0 : (j == 2 ? s1 : s2);
+    const uint32_t hi = j < 2 ? s1 : s2;
+    return __builtin_amdgcn_alignbit(hi, lo, (32u - 8u * j) & 31u);   // bits 24j.. of s2:s1:s0
 }
 
 // Q8_0 scale decode of shaders/gemm_q8_0.wgsl:33-60: exact, but exponent 31

@@ -158,6 +158,33 @@ void q5k_pack_high_bits(uint8_t *blk) {
     }
 }
 
+// The 12 GGML scale bytes of a Q4_K / Q5_K super-block (6-bit sc and m of
+// the 8 sub-blocks, get_scale_min_k4's packing) rewritten in place as the
+// chunk-pair fields of kq_group: field j (bits 24j .. 24j + 23 of bytes
+// 4..15, little-endian) = sc(2j) | sc(2j+1) << 6 | m(2j) << 12 | m(2j+1) << 18.
+void kquant_pack_scales(uint8_t *blk) {
+    uint8_t s[12];
+    std::memcpy(s, blk + 4, 12);
+    uint32_t sc[8], mn[8];
+    for (int i = 0; i < 8; ++i) {
+        if (i < 4) {
+            sc[i] = s[i] & 63u;
+            mn[i] = s[i + 4] & 63u;
+        } else {
+            sc[i] = (s[i + 4] & 15u) | ((uint32_t)(s[i - 4] >> 6) << 4);
+            mn[i] = (uint32_t)(s[i + 4] >> 4) | ((uint32_t)(s[i] >> 6) << 4);
+        }
+    }
+    uint32_t w[3] = {0u, 0u, 0u};
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t f = sc[2 * j] | (sc[2 * j + 1] << 6) | (mn[2 * j] << 12) | (mn[2 * j + 1] << 18);
+        const int bit = 24 * j, wi = bit / 32, sh = bit % 32;
+        w[wi] |= f << sh;
+        if (sh + 24 > 32) w[wi + 1] |= f >> (32 - sh);
+    }
+    for (int i = 0; i < 12; ++i) blk[4 + i] = (uint8_t)(w[i / 4] >> (8 * (i % 4)));
+}
+
 // ---- dequantisation kernels (debug/bit-exactness entry) --------------------
 
 __global__ void dequant_q4_0_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ sc,
@@ -181,14 +208,12 @@ __global__ void dequant_q8_0_kernel(const uint8_t *__restrict__ qs, const uint16
     for (int j = 0; j < 32; ++j) out[b * 32 + j] = d * (float)q[j];
 }
 
-__device__ __forceinline__ void q4k_scale_min(const uint8_t *s, int j, int &sc, int &mn) {
-    if (j < 4) {
-        sc = s[j] & 63;
-        mn = s[j + 4] & 63;
-    } else {
-        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-    }
+// sc and m of sub-block i from the packed scale words at blk + 4.
+__device__ __forceinline__ void q4k_scale_min(const uint8_t *s, int i, int &sc, int &mn) {
+    const uint32_t *w = (const uint32_t *)s;
+    const uint32_t g = kq_group(w[0], w[1], w[2], (uint32_t)i >> 1), o = 6u * (uint32_t)(i & 1);
+    sc = (int)((g >> o) & 63u);
+    mn = (int)((g >> (12u + o)) & 63u);
 }
 
 __global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ blocks, float *__restrict__ out,
@@ -493,8 +518,10 @@ int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const 
         size_t nblk = elems / 256;
         if (nbytes != nblk * bb) return fail(ctx, JANUS_E_INVALID_DIM, "K-quant tensor byte size mismatch");
         qs.assign(src, src + nbytes);
-        if (q5)
-            for (size_t b = 0; b < nblk; ++b) q5k_pack_high_bits(qs.data() + b * bb);
+        for (size_t b = 0; b < nblk; ++b) {
+            kquant_pack_scales(qs.data() + b * bb);
+            if (q5) q5k_pack_high_bits(qs.data() + b * bb);
+        }
         if (ftz)
             for (size_t b = 0; b < nblk; ++b) {
                 uint8_t *blk = qs.data() + b * bb;

@@ -17,7 +17,8 @@
 //     e0,e2,e4,e6,e1,e3,e5,e7 so that (w >> 4t) & 0x000f000f yields the
 //     natural pair (e_2t, e_2t+1) as binary16 1024 + q.
 //     Q4_0 side data: [g][c][32] u32 = the two blocks' binary16 scales.
-//     Q4_K side data: [g][super-block][32] 16-byte headers (d, dmin, scales).
+//     Q4_K side data: [g][super-block][32] 16-byte headers as uploaded (d,
+//     dmin, scale fields of kq_group).
 //   Q5_K: as Q4_K (nibbles and headers), plus the fifth bits: one word per
 //     lane and chunk [g][c][64], bit 4 * slot + i for the element in nibble
 //     slot `slot` of the lane's word i (176 bytes per 256 weights, the GGUF
@@ -243,20 +244,11 @@ struct GQ4_K {
         w.hdr = *(const uint4 *)(a.side + (sb * 32 + (lane & 31)) * 16);
         return w;
     }
+    // (sc, m) of sub-block `sub` (uniform) from the packed scale words hdr.y..w
     __device__ static void scale_min(const uint4 &hdr, int sub, float &sc, float &mn) {
-        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-        uint32_t scv, mnv;
-        if (sub < 4) {
-            scv = (s0 >> (8 * sub)) & 63u;
-            mnv = (s1 >> (8 * sub)) & 63u;
-        } else {
-            const int i = sub - 4;
-            const uint32_t b8 = (s2 >> (8 * i)) & 0xffu;
-            scv = (b8 & 15u) | ((((s0 >> (8 * i)) & 0xffu) >> 6) << 4);
-            mnv = (b8 >> 4) | ((((s1 >> (8 * i)) & 0xffu) >> 6) << 4);
-        }
-        sc = (float)scv;
-        mn = (float)mnv;
+        const uint32_t g = kq_group(hdr.y, hdr.z, hdr.w, (uint32_t)sub >> 1), o = 6u * (uint32_t)(sub & 1);
+        sc = (float)((g >> o) & 63u);
+        mn = (float)((g >> (12u + o)) & 63u);
     }
     template <int MT>
     __device__ static void mma(const W &w, const _Float16 *As, uint32_t pitch, uint32_t kl, int lane,

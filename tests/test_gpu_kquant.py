@@ -1,5 +1,7 @@
-"""GPU parity of the Q5_K and Q6_K weight formats.
+"""GPU parity of the K-quant weight formats.
 
+- Q4_K / Q5_K: the scale fields the upload rewrites decode every byte value
+  of the GGML scale bytes as get_scale_min_k4 does.
 - Q6_K: the upload dequantises on the host to binary16 as the reference's
   loader does (compute/engine.rs:800-831) and the handle reports F16; the
   stored weights are bit-exact against the oracle's dequantisation rounded
@@ -118,3 +120,46 @@ def test_q5_k_model_fused_and_batched_paths(engine):
     assert _rel_err(singles[1], want) <= REL
     assert _rel_err(out[1], want) <= REL
     mb.close()
+
+
+def _every_scale_byte(ggml_type, seed):
+    """Q4_K / Q5_K bytes over 8 rows of 32 super-blocks in which scale byte i
+    (bytes 4..15) of super-block b is (b + 97 i) % 256: every position takes
+    every byte value once, so every 6-bit sc and m of every sub-block, with
+    its top bits from the shared bytes of sub-blocks 4..7, is decoded."""
+    n, k = 8, 32 * 256
+    rng = np.random.default_rng(seed)
+    bb = 144 if ggml_type == _lib.DT_Q4_K else 176
+    nsb = n * k // 256
+    raw = np.frombuffer(rng.bytes(nsb * bb), np.uint8).reshape(nsb, bb).copy()
+    dd = np.abs(rng.standard_normal((nsb, 2), dtype=np.float32)) * np.float32(0.02 / 128)
+    raw[:, 0:4] = synth.f16_bits(dd).view(np.uint8).reshape(nsb, 4)
+    b = np.arange(nsb)[:, None]
+    raw[:, 4:16] = ((b + 97 * np.arange(12)[None, :]) % 256).astype(np.uint8)
+    return n, k, raw.reshape(-1)
+
+
+@pytest.mark.parametrize("ggml_type", [_lib.DT_Q4_K, _lib.DT_Q5_K])
+def test_k_scale_fields_every_byte_value(engine, ggml_type):
+    """The upload rewrites the 12 scale bytes as one 24-bit field per chunk
+    pair; dequantisation is bit-exact against the oracle's GGML decode
+    (get_scale_min_k4) for every byte value in every position, and the M = 1
+    product and the 4-row MFMA product stay within 2e-5 * sum |w x| of the
+    f64 product over those weights."""
+    n, k, raw = _every_scale_byte(ggml_type, 40 + ggml_type)
+    w = ops.GpuTensor(engine, ggml_type, n, k, raw)
+    got = w.dequant().cpu().numpy()
+    want = O.dequant(ggml_type, raw, n, k)
+    assert np.array_equal(got.reshape(-1).view(np.uint32), want.reshape(-1).view(np.uint32))
+    wf = want.reshape(n, k).astype(np.float64)
+    x = np.random.default_rng(7).standard_normal(k, dtype=np.float32)
+    y = torch.empty(n, device=DEV)
+    ops.gemm_auto(engine, torch.from_numpy(x).to(DEV), w, y, 1, 1, k, n)
+    bound = 2e-5 * (np.abs(wf) @ np.abs(x.astype(np.float64))) + 1e-30
+    assert np.all(np.abs(y.cpu().numpy() - wf @ x.astype(np.float64)) <= bound)
+    a16 = torch.from_numpy(np.random.default_rng(8).standard_normal((4, k), dtype=np.float32)).to(torch.float16)
+    c = torch.empty(4, n, device=DEV)
+    ops.gemm_auto(engine, a16.to(DEV), w, c, 4, 1, k, n)
+    xa = a16.float().numpy().astype(np.float64)
+    bound = 2e-5 * (np.abs(xa) @ np.abs(wf).T) + 1e-30
+    assert np.all(np.abs(c.cpu().numpy() - xa @ wf.T) <= bound)
