@@ -150,6 +150,15 @@ __device__ __forceinline__ jh2 nib_hi(uint32_t u, uint32_t m6400, _Float16 off) 
     return __builtin_elementwise_fma(as_h2((u & 0x00f000f0u) | m6400), s16, c);   // (1024 + 16 q) / 16 + 960 - off
 }
 
+// Bytes 2S and 2S + 1 of v, each below 16, as the exact binary16 integers
+// (natural pair order). A byte b < 16 read as OCP e4m3 is b * 2^-9 (the
+// subnormals m * 2^-9 below 8, the lowest normal binade (8 + m) * 2^-9 from
+// 8), and v_cvt_scalef32_pk_f16_fp8 scales it by 512 exactly: one instruction
+// per pair against an AND-OR plus a packed add or FMA for the 0x6400 form.
+template <bool S> __device__ __forceinline__ jh2 nib8(uint32_t v) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 512.0f, S);
+}
+
 // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3): the pair order the nibble unpack produces.
 __device__ __forceinline__ void perm4(uint32_t w01, uint32_t w23, jh2 &even, jh2 &odd) {
     even = as_h2(__builtin_amdgcn_perm(w23, w01, 0x05040100u));
@@ -167,6 +176,26 @@ __device__ __forceinline__ float load16h_perm(const _Float16 *p, jh2 *dst) {
         uint4 t = q[i];
         perm4(t.x, t.y, dst[4 * i + 0], dst[4 * i + 1]);
         perm4(t.z, t.w, dst[4 * i + 2], dst[4 * i + 3]);
+        s0 = dot2(as_h2(t.x), one, s0);
+        s1 = dot2(as_h2(t.y), one, s1);
+        s0 = dot2(as_h2(t.z), one, s0);
+        s1 = dot2(as_h2(t.w), one, s1);
+    }
+    return s0 + s1;
+}
+
+// 16 halves at p (16-byte aligned) -> 8 pairs in order, plus their fp32 sum.
+__device__ __forceinline__ float load16h(const _Float16 *p, jh2 *dst) {
+    const uint4 *q = (const uint4 *)p;
+    const jh2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint4 t = q[i];
+        dst[4 * i + 0] = as_h2(t.x);
+        dst[4 * i + 1] = as_h2(t.y);
+        dst[4 * i + 2] = as_h2(t.z);
+        dst[4 * i + 3] = as_h2(t.w);
         s0 = dot2(as_h2(t.x), one, s0);
         s1 = dot2(as_h2(t.y), one, s1);
         s0 = dot2(as_h2(t.z), one, s0);
@@ -227,7 +256,7 @@ __device__ void stage_x(const XIN *__restrict__ x, uint32_t k, XT *xs, float *sx
 struct FQ4_0 {
     static constexpr int UNIT = 32;
     static constexpr bool XREREAD = false;   // long rows re-read x from LDS per row group
-    static constexpr bool PERM = true;
+    static constexpr bool PERM = false;      // binary16 x staged in element order (nib8 pairs)
     struct W { uint4 q; uint16_t d; };
     __device__ static W load(WPtr w, size_t unit) {
         W r;
@@ -279,9 +308,9 @@ struct FQ4_0 {
         }
         return h2f(w.d) * (s0 + s1);
     }
-    // x[0..32) as pairs (the offset is in the unpacked weights, so no sum of x)
-    struct XH { jh2 v[16]; };
-    __device__ static XH loadx(const _Float16 *xs, const float *, int u) {
+    // x[0..32) as pairs in element order and the sums of its two halves
+    struct XH { jh2 v[16]; float s0, s1; };
+    __device__ static XH loadx(const _Float16 *xs, const float *sx16, int u) {
         XH r;
         const uint4 *p = (const uint4 *)(xs + u * XLayout<_Float16>::STRIDE);
 #pragma unroll
@@ -292,6 +321,8 @@ struct FQ4_0 {
             r.v[4 * i + 2] = as_h2(t.z);
             r.v[4 * i + 3] = as_h2(t.w);
         }
+        r.s0 = sx16[2 * u];
+        r.s1 = sx16[2 * u + 1];
         return r;
     }
     // register-resident x, read straight from global memory
@@ -309,31 +340,26 @@ struct FQ4_0 {
     }
     __device__ static XH loadx_g(const _Float16 *x, int u) {
         XH r;
-        (void)load16h_perm(x + (size_t)u * 32, r.v);
-        (void)load16h_perm(x + (size_t)u * 32 + 16, r.v + 8);
+        r.s0 = load16h(x + (size_t)u * 32, r.v);
+        r.s1 = load16h(x + (size_t)u * 32 + 16, r.v + 8);
         return r;
     }
-    // Each nibble pair becomes the exact binary16 integers q - 8 (nib_lo /
-    // nib_hi: one AND-OR and one packed add or FMA per pair), so every
-    // v_dot2_f32_f16 product is exact; the low- and high-nibble chains are
-    // added once per block and scaled by d.
+    // Each nibble pair becomes the exact binary16 integers q (nib8), so every
+    // v_dot2_f32_f16 product is exact; the offset enters as -8 * sum(x) at
+    // the head of each chain (low nibbles: x[0..16), high: x[16..32)), and
+    // the two chains are added once per block and scaled by d.
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-        const uint32_t m = vgpr_const_6400();
-        const _Float16 off = (_Float16)1032.0f;
         float s = 0.0f, t = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = q[i], u8 = u >> 8;
-            const jh2 a = nib_lo(u, m, off);    // (4i, 4i+2)
-            const jh2 c = nib_lo(u8, m, off);   // (4i+1, 4i+3)
-            const jh2 b = nib_hi(u, m, off);    // (16+4i, 16+4i+2)
-            const jh2 e = nib_hi(u8, m, off);   // (16+4i+1, 16+4i+3)
-            // x pairs (permuted staging): v[2g] = (x[4g], x[4g+2]), v[2g+1] = (x[4g+1], x[4g+3])
-            s = i == 0 ? dot2z(a, x.v[0]) : dot2(a, x.v[2 * i], s);
-            t = i == 0 ? dot2z(b, x.v[8]) : dot2(b, x.v[8 + 2 * i], t);
-            s = dot2(c, x.v[2 * i + 1], s);
-            t = dot2(e, x.v[8 + 2 * i + 1], t);
+            const uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            // (4i, 4i+1) and (16+4i, 16+4i+1); the chain heads keep -8 * sum
+            // intact (x and its sums are often loop-invariant)
+            s = i == 0 ? dot2a(nib8<false>(lo), x.v[0], -8.0f * x.s0) : dot2(nib8<false>(lo), x.v[2 * i], s);
+            t = i == 0 ? dot2a(nib8<false>(hi), x.v[8], -8.0f * x.s1) : dot2(nib8<false>(hi), x.v[8 + 2 * i], t);
+            s = dot2(nib8<true>(lo), x.v[2 * i + 1], s);     // (4i+2, 4i+3)
+            t = dot2(nib8<true>(hi), x.v[8 + 2 * i + 1], t);
         }
         return h2f(w.d) * (s + t);
     }
@@ -410,7 +436,7 @@ struct FQ8_0 {
 struct FQ4_K {
     static constexpr int UNIT = 32;
     static constexpr bool XREREAD = true;   // long rows re-read x from LDS per row group
-    static constexpr bool PERM = true;
+    static constexpr bool PERM = false;     // binary16 x staged in element order (nib8 pairs)
     // The 16-byte super-block header (d, dmin, the scale fields of kq_group
     // in words 1-3) is shared by the 8 units of a super-block, which sit on 8
     // consecutive lanes in every kernel, unit c on lane p = lane & 7 (units
@@ -497,8 +523,8 @@ struct FQ4_K {
         int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
         const _Float16 *base = x + (size_t)sb * 256 + 64 * j + 16 * h;
         XH r;
-        r.slo = load16h_perm(base, r.lo);
-        r.shi = load16h_perm(base + 32, r.hi);
+        r.slo = load16h(base, r.lo);
+        r.shi = load16h(base + 32, r.hi);
         return r;
     }
     template <class WW, class X>
@@ -533,24 +559,17 @@ struct FQ4_K {
         }
         return finish(w, x, l0 + l1, h0 + h1);
     }
-    // Nibbles as the exact binary16 integers q (nib_lo / nib_hi with no
-    // offset, see FQ4_0).
+    // Nibbles as the exact binary16 integers q (nib8, pairs in element order).
     __device__ static float dot(const W &w, const XH &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-        const uint32_t m = vgpr_const_6400();
-        const _Float16 off = (_Float16)1024.0f;
         float l = 0.0f, h = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = q[i], u8 = u >> 8;
-            const jh2 a = nib_lo(u, m, off);
-            const jh2 c = nib_lo(u8, m, off);
-            const jh2 b = nib_hi(u, m, off);
-            const jh2 e = nib_hi(u8, m, off);
-            l = i == 0 ? dot2z(a, x.lo[0]) : dot2(a, x.lo[2 * i], l);
-            h = i == 0 ? dot2z(b, x.hi[0]) : dot2(b, x.hi[2 * i], h);
-            l = dot2(c, x.lo[2 * i + 1], l);
-            h = dot2(e, x.hi[2 * i + 1], h);
+            const uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            l = i == 0 ? dot2z(nib8<false>(lo), x.lo[0]) : dot2(nib8<false>(lo), x.lo[2 * i], l);
+            h = i == 0 ? dot2z(nib8<false>(hi), x.hi[0]) : dot2(nib8<false>(hi), x.hi[2 * i], h);
+            l = dot2(nib8<true>(lo), x.lo[2 * i + 1], l);
+            h = dot2(nib8<true>(hi), x.hi[2 * i + 1], h);
         }
         return finish(w, x, l, h);
     }
@@ -564,6 +583,18 @@ struct FQ4_K {
 // quant byte t, so (w >> i) & 0x01010101 sits under the bytes of quant word
 // i. Weight = (d*sc)*q - dmin*m with q in 0..31.
 struct FQ5_K : FQ4_K {
+    // 5-bit values do not fit e4m3's linear range: the 0x6400 form, whose
+    // pairs are (x[i], x[i+2]), so binary16 x is staged permuted.
+    static constexpr bool PERM = true;
+    using FQ4_K::loadx_g;
+    __device__ static XH loadx_g(const _Float16 *x, int u) {
+        int sb = u >> 3, c = u & 7, j = c >> 1, h = c & 1;
+        const _Float16 *base = x + (size_t)sb * 256 + 64 * j + 16 * h;
+        XH r;
+        r.slo = load16h_perm(base, r.lo);
+        r.shi = load16h_perm(base + 32, r.hi);
+        return r;
+    }
     struct W { uint4 q; uint32_t qh; uint32_t hw; };
     __device__ static W load_row(WPtr w, size_t ru, uint32_t u) {
         const uint8_t *row = w.qs + (ru >> 3) * 176;   // uniform; one 32-bit lane offset per load
