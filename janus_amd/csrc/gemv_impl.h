@@ -872,7 +872,8 @@ __device__ __forceinline__ float reduce_wave_rows(float (&v)[R], int lane, int &
 template <class F, typename XT, int BPL, int R, bool FULL, int XMODE = 0, class StageFn = int, bool DB = true,
           class PreFn = int>
 __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = nullptr,
-                                              const float *sx16 = nullptr, StageFn stage = 0, PreFn pre = 0) {
+                                              const float *sx16 = nullptr, StageFn stage = 0, PreFn pre = 0,
+                                              uint64_t *lbest = nullptr) {
     const int lane = threadIdx.x & 63;
     // wavefront-uniform: row bases then live in scalar registers
     const uint32_t wg_waves = a.threads >> 6;
@@ -1097,7 +1098,25 @@ __device__ __forceinline__ void gemv_reg_body(const GemvArgs &a, const XT *xs = 
                                    (uint32_t)shfl_xor((int)(best & 0xffffffffu), o);
             best = other > best ? other : best;
         }
-        if (lane == 0 && best) atomicMax(a.best, (unsigned long long)best);
+        if (lane == 0) {
+            if (lbest) {
+                // Workgroup maximum in LDS (lbest[0], zeroed by the staging
+                // before its barrier, with the arrival count in lbest[1]); the
+                // last of the workgroup's wavefronts that own groups folds it
+                // into the global key: one global atomic per workgroup.
+                const uint32_t wg0 = blockIdx.x * wg_waves;
+                const uint32_t owners = groups > wg0 ? min(wg_waves, groups - wg0) : 0u;
+                __hip_atomic_fetch_max(lbest, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const uint64_t n = __hip_atomic_fetch_add(lbest + 1, (uint64_t)1, __ATOMIC_ACQ_REL,
+                                                          __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (n + 1 == owners) {
+                    const uint64_t wb = __hip_atomic_load(lbest, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (wb) atomicMax(a.best, (unsigned long long)wb);
+                }
+            } else if (best) {
+                atomicMax(a.best, (unsigned long long)best);
+            }
+        }
     }
 }
 
@@ -1400,6 +1419,7 @@ __global__ __launch_bounds__((lds_max_threads<F, BPL>())) void gemv_lds_kernel(G
     _Float16 *xs = (_Float16 *)smem;
     float *sx16 = (float *)(smem + ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~15u));
     float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
+    uint64_t *lbest = (uint64_t *)(red + 16);   // folded argmax key and arrival count
     NormRegs<NORM_MAXG> nr;
     // Plain binary16 x is requested first too, except on long K-quant and F16
     // rows (no registers to spare there)
@@ -1420,6 +1440,7 @@ __global__ __launch_bounds__((lds_max_threads<F, BPL>())) void gemv_lds_kernel(G
         } else {
             stage_x16<F::PERM, false>(a.x, a.k, nt, xs, sx16, nullptr, 1.0f);
         }
+        if (threadIdx.x == 0) lbest[0] = lbest[1] = 0;
         __syncthreads();
     };
     constexpr int XMODE = BPL <= 4 ? 1 : 2;
@@ -1431,9 +1452,11 @@ __global__ __launch_bounds__((lds_max_threads<F, BPL>())) void gemv_lds_kernel(G
     // with x first 9.05 us)
     constexpr bool DB = BPL <= 4 || (!F::XREREAD && !XPRE);
     if (a.units == 64u * BPL)
-        gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+        gemv_reg_body<F, _Float16, BPL, R, true, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre,
+                                                                                           lbest);
     else
-        gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+        gemv_reg_body<F, _Float16, BPL, R, false, XMODE, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre,
+                                                                                            lbest);
 }
 
 // The LDS-staged product on binary32 x (the reference's dtype; the fused
@@ -1449,6 +1472,7 @@ __global__ __launch_bounds__(512) void gemv_lds32_kernel(GemvArgs a) {
     float *xs = (float *)smem;
     float *sx16 = (float *)(smem + ((nblk * XLayout<float>::STRIDE * 4 + 15) & ~15u));
     float *red = sx16 + (((a.k + 15) / 16 + 3) & ~3u);
+    uint64_t *lbest = (uint64_t *)(red + 16);   // folded argmax key and arrival count
     NormRegs<NORM_MAXG> nr;
     X32Regs xr;
     const uint32_t nt = a.threads;
@@ -1461,13 +1485,14 @@ __global__ __launch_bounds__(512) void gemv_lds32_kernel(GemvArgs a) {
         if constexpr (NORM) stage_x32_norm<NORM_MAXG>(nr, a.k, nt, xs, sx16, a.eps, red);
         else if (xpre) x32_store(xr, a.k, nt, xs, sx16);
         else stage_x<float, float, false>((const float *)a.x, a.k, xs, sx16, (int)nt);
+        if (threadIdx.x == 0) lbest[0] = lbest[1] = 0;
         __syncthreads();
     };
     constexpr bool DB = BPL <= 4;
     if (a.units == 64u * BPL)
-        gemv_reg_body<F, float, BPL, R, true, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+        gemv_reg_body<F, float, BPL, R, true, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre, lbest);
     else
-        gemv_reg_body<F, float, BPL, R, false, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre);
+        gemv_reg_body<F, float, BPL, R, false, 2, decltype(stage), DB, decltype(pre)>(a, xs, sx16, stage, pre, lbest);
 }
 
 // Generic fallback for F16 weights whose k is not a multiple of 8: one
@@ -1607,7 +1632,7 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     static std::atomic<int> per_cu[2][17][17] = {};   // relaxed, as in launch_reg
     const void *kern = norm ? (const void *)gemv_lds_kernel<F, BPL, R, true> : (const void *)gemv_lds_kernel<F, BPL, R, false>;
     const uint32_t nblk = (a.k + XB - 1) / XB;
-    const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
+    const size_t lds = ((nblk * XLayout<_Float16>::STRIDE * 2 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 80;
     if (lds > 64 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for LDS staging");
     const size_t lds_step = (lds + 4095) / 4096;
     std::atomic<int> &occ_cache = per_cu[norm ? 1 : 0][wg_waves][lds_step];
@@ -1639,7 +1664,7 @@ int launch_lds32(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     const int threads = 512, wg_waves = 8;
     const uint32_t groups = (a.n + R - 1) / R;
     const uint32_t nblk = (a.k + XB - 1) / XB;
-    const size_t lds = ((nblk * XLayout<float>::STRIDE * 4 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 64;
+    const size_t lds = ((nblk * XLayout<float>::STRIDE * 4 + 15) & ~(size_t)15) + ((((a.k + 15) / 16) + 3) & ~3u) * 4 + 80;
     if (lds > 160 * 1024) return janus::fail(ctx, JANUS_E_INVALID_DIM, "gemv: k too large for f32 LDS staging");
     const void *kern = norm ? (const void *)gemv_lds32_kernel<F, BPL, R, true> : (const void *)gemv_lds32_kernel<F, BPL, R, false>;
     static const bool attr_set = [] {   // > 64 KiB of dynamic LDS for long rows; thread-safe one-time set-up
