@@ -1615,18 +1615,22 @@ template <class F, int BPL, int R>
 int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
     constexpr int TMAX = lds_max_threads<F, BPL>();
     const uint32_t groups = (a.n + R - 1) / R;
-    // At most one row group per wavefront (16 per CU): one workgroup per CU
-    // with a wavefront per group, x staged once per CU (Q4_0 4096x4096 in
-    // 1024 threads 4.0 -> 3.7 us; the fused QKV's 3072 groups in 768 threads
-    // 6.8 -> 6.4). More groups: 512-thread workgroups, two per CU, whose
-    // stagings and barriers do not hold each other's wavefronts (Q4_0
-    // 14336x4096 7.8 -> 7.35 us, gate/up 28672x4096 14.6 -> 13.2).
+    // Q4_0 / F16 rows of one or two units per lane in at most 16 row groups
+    // per CU (batch-1 QKV and o-proj): one 512-thread workgroup per CU, so a
+    // wavefront owns about two groups (the second group's weights are
+    // requested before the first is consumed) and x is staged once per CU.
+    // Otherwise 512-thread workgroups, two per CU, whose stagings and
+    // barriers do not hold each other's wavefronts (Q4_0 14336x4096 7.8 ->
+    // 7.35 us, gate/up 28672x4096 14.6 -> 13.2; K-quant rows, VALU-heavier,
+    // and the long down-proj rows measured slower at one per CU).
+    // JANUS_GEMV_LDS_THREADS sets the size (up to 1024 where the body fits)
+    // and the JANUS_GEMV_LDS_WPC cap applies to it.
     int threads = 512;
-    if (TMAX == 1024 && groups <= 16u * ctx->num_cus) {
-        const uint32_t w = (groups + ctx->num_cus - 1) / ctx->num_cus;   // wavefronts for one workgroup per CU
-        threads = w <= 8 ? 512 : (int)(64 * w);
+    int one_per_cu = TMAX == 1024 && groups <= 16u * ctx->num_cus;
+    if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) {
+        threads = (int)ctx->gemv_lds_threads;
+        one_per_cu = 0;
     }
-    if (ctx->gemv_lds_threads && (int)ctx->gemv_lds_threads <= TMAX) threads = (int)ctx->gemv_lds_threads;
     const int wg_waves = threads / 64;
     // resident workgroups per CU for this kernel at this LDS size (4 KB steps)
     static std::atomic<int> per_cu[2][17][17] = {};   // relaxed, as in launch_reg
@@ -1644,7 +1648,7 @@ int launch_lds(janus_ctx *ctx, const GemvArgs &a, bool norm) {
         occ = nb;
         occ_cache.store(occ, std::memory_order_relaxed);
     }
-    const int wg_cap = (int)ctx->gemv_lds_wpc / wg_waves;
+    const int wg_cap = one_per_cu ? 1 : (int)ctx->gemv_lds_wpc / wg_waves;
     int pc = occ < wg_cap ? occ : wg_cap;
     if (pc < 1) pc = 1;
     uint32_t blocks = (groups + wg_waves - 1) / wg_waves;
