@@ -815,16 +815,16 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
 
 void janus_model_destroy(janus_model *m) {
     if (!m) return;
-    hipStreamSynchronize(m->ctx->stream);
+    (void)hipStreamSynchronize(m->ctx->stream);
     free_graphs(m);
-    if (m->cap_stream) hipStreamDestroy(m->cap_stream);
+    if (m->cap_stream) (void)hipStreamDestroy(m->cap_stream);
     for (hipEvent_t ev : m->stream_ev)
-        if (ev) hipEventDestroy(ev);
-    if (m->h_stream) hipHostFree(m->h_stream);
+        if (ev) (void)hipEventDestroy(ev);
+    if (m->h_stream) (void)hipHostFree(m->h_stream);
     for (auto &L : m->layers) {
         for (janus_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down, L.qkv, L.gu}) janus_weight_free(m->ctx, w);
-        hipFree(L.attn_norm);
-        hipFree(L.ffn_norm);
+        (void)hipFree(L.attn_norm);
+        (void)hipFree(L.ffn_norm);
     }
     janus_weight_free(m->ctx, m->tok_embd);
     janus_weight_free(m->ctx, m->lm_head);
@@ -834,7 +834,7 @@ void janus_model_destroy(janus_model *m) {
                     (void *)m->rope, (void *)m->d_pos, (void *)m->d_lens, (void *)m->d_tokens, (void *)m->d_feed, (void *)m->d_rowbase,
                     (void *)m->d_rows, (void *)m->d_prompts, (void *)m->d_out, (void *)m->d_counts,
                     (void *)m->d_best, (void *)m->d_sampler})
-        if (p) hipFree(p);
+        if (p) (void)hipFree(p);
     delete m;
 }
 
@@ -866,7 +866,7 @@ int janus_model_set_tensor(janus_model *m, const char *cname, int type, uint32_t
         *dst = w;
         return JANUS_OK;
     };
-    hipStreamSynchronize(ctx->stream);
+    JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
     free_graphs(m);
     m->fused_ready = false;
     m->tiles_ready = false;
@@ -945,8 +945,8 @@ int janus_model_set_kv_cache(janus_model *m, void *d_k, void *d_v, size_t bytes_
     JANUS_HIP_CHECK(m->ctx, hipStreamSynchronize(m->ctx->stream));
     free_graphs(m);
     if (!m->kv_external) {
-        hipFree(m->kcache);
-        hipFree(m->vcache);
+        (void)hipFree(m->kcache);
+        (void)hipFree(m->vcache);
     }
     m->kcache = d_k;
     m->vcache = d_v;

@@ -116,11 +116,11 @@ namespace {
 struct DeviceGuard {
     int prev = -1;
     explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) == hipSuccess && prev != dev) hipSetDevice(dev);
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) (void)hipSetDevice(dev);
         else prev = -1;
     }
     ~DeviceGuard() {
-        if (prev >= 0) hipSetDevice(prev);
+        if (prev >= 0) (void)hipSetDevice(prev);
     }
 };
 
@@ -387,12 +387,12 @@ void janus_destroy(janus_ctx *ctx) {
         return;
     }
     DeviceGuard g(ctx->device);
-    if (ctx->own_stream) hipStreamSynchronize(ctx->own_stream);
-    if (ctx->stream && ctx->stream != ctx->own_stream) hipStreamSynchronize(ctx->stream);
-    if (ctx->attn_ws) hipFree(ctx->attn_ws);
-    if (ctx->gemm_ws) hipFree(ctx->gemm_ws);
-    for (void *p : ctx->retired) hipFree(p);
-    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
+    if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+    if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    for (void *p : ctx->retired) (void)hipFree(p);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
 
@@ -593,7 +593,7 @@ int janus_weight_upload(janus_ctx *ctx, int type, uint32_t n, uint32_t k, const 
     if (e == hipSuccess && !sc.empty())
         e = hipMemcpy((void *)w->sc, sc.data(), sc.size() * 2, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-        hipFree(w->base);
+        (void)hipFree(w->base);
         delete w;
         return hip_fail(ctx, e, "hipMemcpy(weight)");
     }
@@ -605,10 +605,10 @@ int janus_weight_free(janus_ctx *ctx, janus_weight *w) {
     if (!w) return JANUS_OK;
     if (ctx && ctx->device >= 0) {
         DeviceGuard g(ctx->device);
-        hipStreamSynchronize(ctx->stream);
+        (void)hipStreamSynchronize(ctx->stream);
     }
-    if (w->base) hipFree(w->base);
-    if (w->t32) hipFree(w->t32);
+    if (w->base) (void)hipFree(w->base);
+    if (w->t32) (void)hipFree(w->t32);
     delete w;
     return JANUS_OK;
 }
