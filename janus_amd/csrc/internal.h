@@ -49,6 +49,7 @@ struct janus_ctx {
     // small-M quantised GEMMs over several K passes per workgroup use the
     // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
     bool gemm_pipe = true;
+    bool epi_split = true;           // batched residual + RMSNorm in two spread launches
     // small-M GEMM pass length / K split forced for every product (0: planned)
     uint32_t gemm_kr = 0, gemm_ks = 0;
     // Attention split-K partials; grows on first use and is then reused.
@@ -175,10 +176,14 @@ int smallm_gemm_launch(janus_ctx *ctx, const void *a, int a_dt, const janus_weig
 bool mfma_gemm_supported(int a_dt, const janus_weight *w);
 int mfma_gemm_prepare(janus_ctx *ctx, const janus_weight *w);
 
-// Split-K partials of one MFMA product: ws[ksplit][mpad][npad] (f32).
+// Split-K partials of one MFMA product: ws[ksplit][mpad][npad] (f32), and
+// beside them in the same workspace a small per-row area for the epilogues
+// (ss: kEpiSlices floats per row).
+constexpr uint32_t kEpiSlices = 16;
 struct GemmPartials {
     const float *ws;
     uint32_t ksplit, mpad, npad;
+    float *ss;
 };
 // Batched products (binary16 rows, 1..64) whose epilogue kernel sums the
 // partials and finishes the step:

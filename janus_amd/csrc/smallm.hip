@@ -1012,9 +1012,11 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     const size_t red = (size_t)WAVES * KW * 16 * 64 * 4;   // K-slice reduction, one M-tile at a time
     if (lds < red) lds = red;
     a.to_ws = parts != nullptr;
+    size_t need = 0;
     if (a.ksplit > 1 || parts) {
-        const size_t need = (size_t)a.ksplit * MT * 32 * G * 32 * 4;
-        if (int e = ensure_gemm_ws(ctx, need)) return e;
+        need = (size_t)a.ksplit * MT * 32 * G * 32 * 4;
+        const size_t epi = parts ? (size_t)MT * 32 * kEpiSlices * 4 : 0;   // the epilogues' per-row area
+        if (int e = ensure_gemm_ws(ctx, need + epi)) return e;
         a.ws = (float *)ctx->gemm_ws;
     }
     static const bool attr_set = [] {   // thread-safe one-time set-up
@@ -1045,6 +1047,7 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
         parts->ksplit = a.ksplit;
         parts->mpad = MT * 32;
         parts->npad = G * 32;
+        parts->ss = a.ws + need / 4;
         return JANUS_OK;
     }
     if (a.ksplit > 1) {
@@ -1203,6 +1206,57 @@ __global__ __launch_bounds__(1024) void epi_resnorm_kernel(GemmPartials p, const
     }
 }
 
+// Residual + RMSNorm spread over the GPU in two launches (a row's sum of
+// squares spans workgroups): epi_ressum_kernel, one 128-thread workgroup per
+// (512-column slice, row), writes out = resid + the summed partials and the
+// slice's sum of squares (threads, then the wavefront by DPP, then the two
+// wavefronts in order) to p.ss[row][slice]; epi_norm_kernel, the same grid,
+// adds the row's slice sums in slice order and writes (x / rms) * gamma as
+// binary16 (activations.wgsl:128, as the M = 1 kernels' fused norm).
+constexpr uint32_t kEpiCols = 512;
+__global__ __launch_bounds__(128) void epi_ressum_kernel(GemmPartials p, const float *resid, float *out,
+                                                         uint32_t hidden) {
+    __shared__ float red[2];
+    const uint32_t m = blockIdx.y, slice = blockIdx.x;
+    const uint32_t i = slice * kEpiCols + 4 * threadIdx.x;
+    const float *q = p.ws + (size_t)m * p.npad;
+    jf4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (i < hidden) {
+        v = sum_splits<jf4>(q + i, (size_t)p.mpad * p.npad, p.ksplit) + *(const jf4 *)(resid + (size_t)m * hidden + i);
+        *(jf4 *)(out + (size_t)m * hidden + i) = v;
+    }
+    float s = fmaf(v.x, v.x, 0.0f);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+    s = wave_sum_dpp(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) p.ss[(size_t)m * kEpiSlices + slice] = red[0] + red[1];
+}
+
+__global__ __launch_bounds__(128) void epi_norm_kernel(GemmPartials p, const float *out,
+                                                       const float *__restrict__ gamma, float eps, _Float16 *xn,
+                                                       uint32_t hidden) {
+    const uint32_t m = blockIdx.y, slice = blockIdx.x;
+    const uint32_t i = slice * kEpiCols + 4 * threadIdx.x;
+    const uint32_t slices = (hidden + kEpiCols - 1) / kEpiCols;
+    // the row and gamma are requested with the slice sums: one round trip
+    jf4 v = {0.0f, 0.0f, 0.0f, 0.0f}, g = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (i < hidden) {
+        v = *(const jf4 *)(out + (size_t)m * hidden + i);
+        g = *(const jf4 *)(gamma + i);
+    }
+    float tot = 0.0f;
+    for (uint32_t t = 0; t < slices; ++t) tot += p.ss[(size_t)m * kEpiSlices + t];
+    const float rms = sqrtf(tot / (float)hidden + eps);
+    if (i < hidden) {
+        const uint32_t lo = (uint32_t)f2h_bits((v.x / rms) * g.x) | ((uint32_t)f2h_bits((v.y / rms) * g.y) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits((v.z / rms) * g.z) | ((uint32_t)f2h_bits((v.w / rms) * g.w) << 16);
+        *(uint2 *)((uint16_t *)xn + (size_t)m * hidden + i) = make_uint2(lo, hi);
+    }
+}
+
 int run_partials(janus_ctx *ctx, const void *a, const janus_weight *w, uint32_t rows, GemmPartials *parts) {
     if (!mfma_gemm_supported(JANUS_DT_F16, w))
         return fail(ctx, JANUS_E_UNSUPPORTED_DTYPE, "batched epilogue: weight has no MFMA path");
@@ -1284,8 +1338,16 @@ int gemm_residual_norm(janus_ctx *ctx, const void *a16, const janus_weight *w, u
         return fail(ctx, JANUS_E_INVALID_DIM, "residual-norm epilogue: rows must be a multiple of 4, at most 8192");
     GemmPartials p{};
     if (int r = run_partials(ctx, a16, w, rows, &p)) return r;
-    const dim3 grid(rows), block(1024);
     _Float16 *xn = (_Float16 *)xn16;
+    if (ctx->epi_split) {
+        const dim3 sgrid((hidden + kEpiCols - 1) / kEpiCols, rows), sblock(kEpiCols / 4);
+        hipLaunchKernelGGL(epi_ressum_kernel, sgrid, sblock, 0, ctx->stream, p, resid, out, hidden);
+        JANUS_LAUNCH_CHECK(ctx);
+        hipLaunchKernelGGL(epi_norm_kernel, sgrid, sblock, 0, ctx->stream, p, out, gamma, eps, xn, hidden);
+        JANUS_LAUNCH_CHECK(ctx);
+        return JANUS_OK;
+    }
+    const dim3 grid(rows), block(1024);
     if (hidden <= 4096) hipLaunchKernelGGL(epi_resnorm_kernel<1>, grid, block, 0, ctx->stream, p, resid, out, gamma, eps, xn, hidden);
     else hipLaunchKernelGGL(epi_resnorm_kernel<2>, grid, block, 0, ctx->stream, p, resid, out, gamma, eps, xn, hidden);
     JANUS_LAUNCH_CHECK(ctx);

@@ -257,3 +257,36 @@ def test_batched_40_sequences_two_m_tiles(engine):
             m.forward([t], [p])
         assert _rel_err(out[s], m.logits()[0]) <= 1e-3, s
         m.close()
+
+
+def test_batched_residual_norm_split_matches_single_workgroup_form(monkeypatch):
+    """The batched residual + RMSNorm epilogue spread over (512-column
+    slice, row) workgroups in two launches against the one-workgroup-per-row
+    kernel (JANUS_EPI_SPLIT=0), at hidden 1152 (three slices, the last one a
+    quarter full), and both against each sequence run alone."""
+    from janus_amd.ops import ComputeEngine
+    spec = synth.make_model(31, 1152, 9, 9, 1024, 1000, 2, synth.Q4_0, 1e-5, 500000.0,
+                            embed_type=synth.F16, head_type=synth.F16)
+    rng = np.random.default_rng(37)
+    lens = [6, 11, 9]
+    prompts = [rng.integers(0, spec.vocab, n).tolist() for n in lens]
+    outs = {}
+    for split in ("0", "1"):
+        monkeypatch.setenv("JANUS_EPI_SPLIT", split)
+        eng = ComputeEngine(0)
+        mb = Model(eng, spec, max_seq_len=32, max_batch=3, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for step in range(max(lens)):
+            mb.forward([pr[min(step, len(pr) - 1)] for pr in prompts], [min(step, len(pr) - 1) for pr in prompts])
+        outs[split] = mb.logits(3)
+        mb.close()
+        if split == "1":
+            for s in range(3):
+                m = Model(eng, spec, max_seq_len=32, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+                for p, t in enumerate(prompts[s]):
+                    m.forward([t], [p])
+                assert _rel_err(outs["1"][s], m.logits()[0]) <= 1e-3
+                m.close()
+        eng.sync()
+        eng.close()
+    for s in range(3):
+        assert _rel_err(outs["1"][s], outs["0"][s]) <= 1e-3
