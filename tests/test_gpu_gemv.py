@@ -91,12 +91,13 @@ def test_gemv_f16_activations(engine, ggml_type, n, k):
     workgroup with five idle wavefronts that stream a real row group and
     discard it. (1003, 4096): F16 with eight units per lane on the
     double-buffered body, five idle wavefronts; the quantised formats two
-    units per lane, one row per step (Q4_0 in 1024-thread workgroups, the
-    rest in 512), idle wavefronts in the last workgroup. (8200, 4096): 8200
-    row groups of one row (quantised formats, 512-thread workgroups), whose
-    persistent grid gives wavefronts a second and third group. (2500, 4096):
-    Q4_0 with ten groups per CU on a 256-CU device, one 640-thread
-    workgroup per CU."""
+    units per lane, one row per step (Q4_0 in one 512-thread workgroup per
+    CU, the K-quants and Q8_0 in two), idle wavefronts in the last workgroup.
+    (8200, 4096): 8200 row groups of one row (quantised formats, 512-thread
+    workgroups two per CU), whose persistent grid gives wavefronts a second
+    and third group. (2500, 4096): Q4_0 with ten groups per CU on a 256-CU
+    device, one 512-thread workgroup per CU whose wavefronts own one or two
+    groups."""
     _check_gemv_f16(engine, ggml_type, n, k)
 
 
@@ -144,12 +145,24 @@ def test_gemv_f16_activations_1024_thread_workgroups(wide_engine, ggml_type, n, 
     _check_gemv_f16(wide_engine, ggml_type, n, k if ggml_type == 2 else k // 4)
 
 
-@pytest.mark.parametrize("n", [2500, 3000])
-def test_gemv_f16_rows_one_workgroup_per_cu(engine, n):
+@pytest.mark.parametrize("n,threads", [(2500, None), (3000, None), (2500, "640"), (3000, "768")])
+def test_gemv_f16_rows_one_workgroup_per_cu(engine, monkeypatch, n, threads):
     """F16 rows of two units per lane (k = 1024), one row per step: 2500 and
-    3000 groups give one workgroup per CU of 640 and 768 threads on a 256-CU
-    device."""
-    _check_gemv_f16(engine, 1, n, 1024)
+    3000 groups run one 512-thread workgroup per CU on a 256-CU device (its
+    wavefronts own one or two groups); with JANUS_GEMV_LDS_THREADS at 640 or
+    768, one such workgroup per CU with about one group per wavefront."""
+    if threads is None:
+        _check_gemv_f16(engine, 1, n, 1024)
+        return
+    from janus_amd.ops import ComputeEngine
+    monkeypatch.setenv("JANUS_GEMV_LDS_THREADS", threads)
+    monkeypatch.setenv("JANUS_GEMV_LDS_WPC", str(int(threads) // 64))
+    eng = ComputeEngine(0)
+    try:
+        _check_gemv_f16(eng, 1, n, 1024)
+    finally:
+        eng.sync()
+        eng.close()
 
 
 def test_gemv_f16_odd_k_generic_path(engine):
