@@ -535,11 +535,9 @@ struct FQ4_K {
         const float d = h2f((uint16_t)(dd & 0xffffu)), dmin = h2f((uint16_t)(dd >> 16));
         const float sl = (float)(g & 63u), sh = (float)((g >> 6) & 63u);
         const float ml = (float)((g >> 12) & 63u), mh = (float)((g >> 18) & 63u);
-        float r = (d * sl) * qlo;
-        r = fmaf(d * sh, qhi, r);
-        r = fmaf(-(dmin * ml), x.slo, r);
-        r = fmaf(-(dmin * mh), x.shi, r);
-        return r;
+        // d (sc_lo q_lo + sc_hi q_hi) - dmin (m_lo sum_lo + m_hi sum_hi)
+        const float a = fmaf(sh, qhi, sl * qlo), b = fmaf(mh, x.shi, ml * x.slo);
+        return fmaf(d, a, -(dmin * b));
     }
     __device__ static float dot(const W &w, const XF &x) {
         const uint32_t q[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
