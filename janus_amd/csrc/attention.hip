@@ -1069,10 +1069,18 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
 }  // namespace
 
 // Splits each sequence's context over wavefronts so the launch has roughly 8
-// wavefronts per CU (at least TP positions each). Contexts of up to 1024
-// positions use 16-wavefront (G <= 2) or 8-wavefront (G = 4) workgroups whose
-// wavefronts merge in LDS, so short contexts need no merge launch; otherwise
-// 4-wavefront workgroups, with a merge kernel across workgroup splits.
+// wavefronts per CU (at least TP positions each). One workgroup per (sequence,
+// head group), its wavefronts merged in LDS and no merge launch, for contexts
+// of up to 512 positions, or up to 1024 when those workgroups fill at least
+// half the CUs; otherwise the context splits over workgroups, with a merge
+// kernel across the splits. Single-sequence attention per call (graph
+// replays, 32 query heads of 128 dims, fp16 cache, plan for the length's
+// bucket): 8 KV heads at 800 / 1500 / 3000 / 6000 positions 7.3 / 7.5 / 10.0 /
+// 13.8 us with per-query-head splits against 9.6 / 11.0 / 15.5 / 18.3 us with
+// one workgroup per head up to 1024 and KV-head splits beyond; 32 KV heads at
+// 640-1024 positions 9.4-10.1 against 11.6-15.5 us with one workgroup per
+// head. Four or eight sequences at 800 positions: 12.5 / 17.0 us with one
+// workgroup per head against 13.8 / 17.9 split.
 void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t hd,
                     uint32_t max_len, int kv_f16, uint32_t *chunk_out, uint32_t *nw_out, uint32_t *splits_out,
                     uint32_t *qh_div_out, uint32_t *rows_out) {
@@ -1082,7 +1090,11 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     // Short contexts with few sequences: one workgroup per query head (the G
     // heads of a KV head re-read its rows from L2) so the launch spreads over
     // G times more CUs and each wavefront does 1/G of the arithmetic.
-    const bool qh = G > 1 && max_len <= 1024 && (uint64_t)batch * heads <= (uint64_t)ctx->num_cus;
+    // Beyond 1024 positions only while batch * heads is at most an eighth of
+    // the CUs (4 sequences of 32 heads at 6000 positions: 70 us per query head
+    // against 29 us per KV head; 1 sequence: 13.8 against 18.3 us).
+    const uint64_t bh = (uint64_t)batch * heads;
+    const bool qh = G > 1 && bh <= (uint64_t)ctx->num_cus && (max_len <= 1024 || 8 * bh <= (uint64_t)ctx->num_cus);
     *qh_div_out = qh ? G : 0;
     const uint64_t waves = (uint64_t)ctx->num_cus * (uint64_t)ctx->attn_wpc;
     // Row streaming (one workgroup per CU over ranges of 16-position blocks):
@@ -1118,12 +1130,18 @@ void attention_plan(const janus_ctx *ctx, uint32_t batch, uint32_t heads, uint32
     const uint64_t groups = (uint64_t)batch * (qh ? heads : kv_heads);
     uint64_t chunk = (max_len * groups + waves - 1) / waves;
     chunk = (chunk + TP - 1) / TP * TP;
-    // per-query-head launches: 8 wavefronts up to 512 positions (bs=1 decode
-    // step at contexts 148-348: 1.458 ms/token against 1.480 with 4 and with
-    // 16), 16 beyond
-    const uint32_t qh_nw = ctx->attn_qh_nw ? ctx->attn_qh_nw : (max_len <= 512 ? 8u : 16u);
-    const uint32_t nw = qh ? qh_nw : (max_len > 1024 ? 4 : (G <= 2 ? 16 : (G == 4 ? 8 : 4)));
-    if (chunk * nw < max_len && max_len <= 1024) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
+    const bool single = max_len <= 512 || (max_len <= 1024 && 2 * groups >= (uint64_t)ctx->num_cus);
+    // per-query-head launches: 8 wavefronts (bs=1 decode step at contexts
+    // 148-348: 1.458 ms/token against 1.480 with 4 and with 16; split
+    // contexts of 520-1024 positions 7.3-7.7 us against 8.0-8.4 with 4), 16
+    // for one workgroup over 513-1024 positions. MHA (G = 1): 4 wavefronts
+    // beyond 256 positions (300-500 positions in one workgroup 6.2-7.1 us
+    // against 6.5-7.7 with 16).
+    uint32_t nw;
+    if (qh) nw = ctx->attn_qh_nw ? ctx->attn_qh_nw : (single && max_len > 512 ? 16u : 8u);
+    else if (max_len > 1024 || !single || (G == 1 && max_len > 256)) nw = 4;
+    else nw = G <= 2 ? 16 : (G == 4 ? 8 : 4);
+    if (single && chunk * nw < max_len) chunk = (max_len + nw * TP - 1) / (nw * TP) * TP;
     *chunk_out = (uint32_t)chunk;
     *nw_out = nw;
     *splits_out = (uint32_t)((max_len + chunk * nw - 1) / (chunk * nw));

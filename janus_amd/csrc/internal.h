@@ -50,6 +50,9 @@ struct janus_ctx {
     // cross-pass pipelined kernel (JANUS_GEMM_PIPE=0 selects the single-buffered one)
     bool gemm_pipe = true;
     bool epi_split = true;           // batched residual + RMSNorm in two spread launches
+    // captured decode steps, one per context-length bucket (JANUS_GRAPH_BUCKETS=0:
+    // one step planned for max_seq_len, for comparisons)
+    bool graph_buckets = true;
     // small-M GEMM pass length / K split forced for every product (0: planned)
     uint32_t gemm_kr = 0, gemm_ks = 0;
     // Attention split-K partials; grows on first use and is then reused.

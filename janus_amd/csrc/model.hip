@@ -85,8 +85,9 @@ struct janus_model {
     unsigned long long *d_best = nullptr;   // greedy key per row (zero between steps)
     SamplerDev *d_sampler = nullptr;
     SamplerDev h_sampler{1.0f, SAMPLE_ARGMAX};
-    // captured steps, one per row count
+    // captured steps, one per row count and length bucket: graphs[nseq * nbuckets + b]
     std::vector<hipGraphExec_t> graphs;
+    uint32_t nbuckets = 1;
     std::vector<uint32_t> h_pos;   // graph_run: host mirror of the rows' positions
     uint32_t graph_nseq = 0;
     hipStream_t cap_stream = nullptr;
@@ -387,12 +388,12 @@ int forward_any(janus_model *m, const uint32_t *h_ids, const int32_t *d_ids, uin
 }
 
 // One full decode step over rows 0..nseq-1 from the device state: forward
-// (every row to max_seq_len capacity), greedy choice (folded into the
-// single-sequence LM head, or keyed over the logits), advance.
-int step_launch(janus_model *m, uint32_t nseq) {
+// (attention planned for rows up to max_len long), greedy choice (folded
+// into the single-sequence LM head, or keyed over the logits), advance.
+int step_launch(janus_model *m, uint32_t nseq, uint32_t max_len) {
     janus_ctx *ctx = m->ctx;
     const bool fold = use_fused1(m, nseq) && can_fold_head(m);
-    int e = forward_any(m, nullptr, m->d_feed, nseq, m->cfg.max_seq_len, fold);
+    int e = forward_any(m, nullptr, m->d_feed, nseq, max_len, fold);
     if (!e && !fold) e = argmax_keys_launch(ctx, m->logits, m->d_best, m->cfg.vocab, nseq, m->d_counts, m->d_sampler);
     if (e) return e;
     AdvanceArgs a;
@@ -485,14 +486,42 @@ void free_graphs(janus_model *m) {
     m->graph_nseq = 0;
 }
 
-// The captured step for nseq rows, captured on first use. Capture follows one
-// eager forward over the same rows (it sets kernel attributes and grows the
-// GEMM workspace outside the capture; it writes the K/V rows the next step
-// writes again with the same values).
-int ensure_graph(janus_model *m, uint32_t nseq) {
-    if (m->graphs[nseq]) return JANUS_OK;
+// Captured steps are planned for a length bucket: the attention of a step
+// whose longest row attends `len` positions runs with the plan for the
+// smallest of 256, 512, 1024, ... (or max_seq_len, the last bucket) that is
+// at least len. A plan for a longer length is correct for any shorter one
+// (lengths are read from the device), so a replay may use any bucket at or
+// above its rows' lengths; the host picks the smallest, from positions it
+// knows to be upper bounds.
+constexpr uint32_t kBucket0 = 256;
+
+uint32_t bucket_count(uint32_t max_seq) {
+    uint32_t n = 1;
+    while (((uint64_t)kBucket0 << (n - 1)) < max_seq) ++n;
+    return n;   // kBucket0 << (n - 2) < max_seq <= INT_MAX, so every bucket length fits
+}
+
+uint32_t bucket_len(const janus_model *m, uint32_t b) {
+    return b + 1 < m->nbuckets ? kBucket0 << b : m->cfg.max_seq_len;
+}
+
+uint32_t bucket_of(const janus_model *m, uint32_t len) {
+    uint32_t b = 0;
+    while (b + 1 < m->nbuckets && (kBucket0 << b) < len) ++b;
+    return b;
+}
+
+// The captured step for nseq rows and length bucket b, captured on first use.
+// Capture follows one eager forward over the same rows (it sets kernel
+// attributes and grows the GEMM workspace outside the capture; it writes the
+// K/V rows the next step writes again with the same values), so it is called
+// only between steps, where the device state is the next step's.
+int ensure_graph(janus_model *m, uint32_t nseq, uint32_t b) {
+    hipGraphExec_t &slot = m->graphs[(size_t)nseq * m->nbuckets + b];
+    if (slot) return JANUS_OK;
     janus_ctx *ctx = m->ctx;
-    if (int e = forward_any(m, nullptr, m->d_feed, nseq, m->cfg.max_seq_len, false)) return e;
+    const uint32_t max_len = bucket_len(m, b);
+    if (int e = forward_any(m, nullptr, m->d_feed, nseq, max_len, false)) return e;
     JANUS_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
     // Capture on the model's own stream (the caller's may be the legacy
     // default stream, which cannot be captured); the graph is launched on the
@@ -505,7 +534,7 @@ int ensure_graph(janus_model *m, uint32_t nseq) {
         ctx->stream = user;
         return hip_fail(ctx, be, "hipStreamBeginCapture");
     }
-    int e = step_launch(m, nseq);
+    int e = step_launch(m, nseq, max_len);
     hipGraph_t g = nullptr;
     hipError_t ce = hipStreamEndCapture(m->cap_stream, &g);
     ctx->stream = user;
@@ -518,7 +547,7 @@ int ensure_graph(janus_model *m, uint32_t nseq) {
     hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (ie != hipSuccess) return hip_fail(ctx, ie, "hipGraphInstantiate");
-    m->graphs[nseq] = ge;
+    slot = ge;
     return JANUS_OK;
 }
 
@@ -529,8 +558,29 @@ int nan_fail(janus_ctx *ctx, uint32_t row) {
                 "GPU returned NaN logits (batch row " + std::to_string(row) + "): no token was sampled");
 }
 
-int replay(janus_model *m, uint32_t nseq, uint32_t steps) {
-    for (uint32_t s = 0; s < steps; ++s) JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(m->graphs[nseq], m->ctx->stream));
+// Captures the steps for nseq rows of every bucket from the one of length
+// lo to the one of length hi.
+int replay_prepare(janus_model *m, uint32_t nseq, uint32_t lo, uint32_t hi) {
+    for (uint32_t b = bucket_of(m, lo), e = bucket_of(m, hi); b <= e; ++b)
+        if (int st = ensure_graph(m, nseq, b)) return st;
+    return JANUS_OK;
+}
+
+// `steps` replays of the captured step for nseq rows. len0 bounds the
+// attention length of the first step's longest row; each step adds at most
+// one position, so step s runs the bucket of min(len0 + s, max_seq_len).
+// Every bucket the replays need is captured before the first is launched.
+int replay(janus_model *m, uint32_t nseq, uint32_t steps, uint32_t len0) {
+    if (!steps) return JANUS_OK;
+    const uint32_t cap = m->cfg.max_seq_len;
+    auto len_at = [&](uint32_t s) -> uint32_t {
+        const uint64_t l = (uint64_t)len0 + s;
+        return l < cap ? (uint32_t)l : cap;
+    };
+    if (int e = replay_prepare(m, nseq, len_at(0), len_at(steps - 1))) return e;
+    hipGraphExec_t *row = &m->graphs[(size_t)nseq * m->nbuckets];
+    for (uint32_t s = 0; s < steps; ++s)
+        JANUS_HIP_CHECK(m->ctx, hipGraphLaunch(row[bucket_of(m, len_at(s))], m->ctx->stream));
     return JANUS_OK;
 }
 
@@ -623,11 +673,11 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
             in.ctl[r] = RowDev{0, 0, 0, 1, EOS_IGNORE, 0};
             in.mask[r / 32] |= 1u << (r % 32);
             parked[r] = 1;
+            hpos[r] = 0;
             any_new = true;
         }
         if (any_new)
             if (int e = set_rows(m, in)) return e;
-        if (int e = ensure_graph(m, nrows)) return e;
         // steps until the first row can be done without an EOS: its prompt,
         // its tokens, or its capacity
         uint32_t k = 16;
@@ -640,7 +690,10 @@ int run_requests(janus_model *m, const std::vector<Request> &reqs, uint32_t max_
             if (need < 1) need = 1;
             if ((uint64_t)need < k) k = (uint32_t)need;
         }
-        if (int e = replay(m, nrows, k)) return e;
+        // hpos holds each row's position (admitted and parked rows start at 0)
+        int32_t top = 0;
+        for (uint32_t r = 0; r < nrows; ++r) top = hpos[r] > top ? hpos[r] : top;
+        if (int e = replay(m, nrows, k, (uint32_t)top + 1)) return e;
         JANUS_HIP_CHECK(ctx, hipMemcpyAsync(hrows.data(), m->d_rows, nrows * sizeof(RowDev), hipMemcpyDeviceToHost,
                                             ctx->stream));
         JANUS_HIP_CHECK(ctx, hipMemcpyAsync(hpos.data(), m->d_pos, nrows * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -688,14 +741,21 @@ int run_stream(janus_model *m, const Request &q, uint32_t max_tokens, janus_toke
     std::vector<int32_t> tmp;
     if (int e = admit_row(m, 0, q, max_tokens, EOS_STOP_DROP, in, tmp)) return e;
     if (int e = set_rows(m, in)) return e;
-    if (int e = ensure_graph(m, 1)) return e;
+    // every bucket the request can reach, captured before the first step so
+    // that no capture stalls the stream of tokens
+    {
+        const uint64_t reach = (uint64_t)q.n + max_tokens + 1;
+        if (int e = replay_prepare(m, 1, 1, reach < m->cfg.max_seq_len ? (uint32_t)reach : m->cfg.max_seq_len))
+            return e;
+    }
     // prefill: positions 0 .. n-1; the last of these steps queues the re-fed
     // last prompt token at position n (or ends the row at max_seq_len)
-    if (int e = replay(m, 1, q.n)) return e;
-    // step i samples token i; at most max_tokens steps can sample one
+    if (int e = replay(m, 1, q.n, 1)) return e;
+    // step i samples token i (the step at position n + i at most); at most
+    // max_tokens steps can sample one
     auto issue = [&](uint32_t i) -> int {
         janus_model::StreamSlot *slot = m->h_stream + (i & 1);
-        if (int e = replay(m, 1, 1)) return e;
+        if (int e = replay(m, 1, 1, q.n + i + 1)) return e;
         JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&slot->row, m->d_rows, sizeof(RowDev), hipMemcpyDeviceToHost, ctx->stream));
         JANUS_HIP_CHECK(ctx, hipMemcpyAsync(&slot->token, m->d_tokens, 4, hipMemcpyDeviceToHost, ctx->stream));
         JANUS_HIP_CHECK(ctx, hipEventRecord(m->stream_ev[i & 1], ctx->stream));
@@ -757,7 +817,8 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
     m->ctx = ctx;
     m->cfg = c;
     m->layers.resize(c.layers);
-    m->graphs.assign(c.max_batch + 1, nullptr);
+    m->nbuckets = ctx->graph_buckets ? bucket_count(c.max_seq_len) : 1;
+    m->graphs.assign((size_t)(c.max_batch + 1) * m->nbuckets, nullptr);
     const size_t B = c.max_batch, kvd = (size_t)c.kv_heads * c.head_dim, S = c.max_seq_len;
     auto alloc = [&](void **p, size_t bytes) { return hipMalloc(p, bytes < 256 ? 256 : bytes) == hipSuccess; };
     bool ok = alloc((void **)&m->hidden, B * c.hidden * 4) && alloc((void **)&m->q, B * c.hidden * 4) &&
@@ -796,14 +857,15 @@ int janus_model_create(janus_ctx *ctx, const janus_model_config *cfg, janus_mode
         janus_model_destroy(m);
         return e;
     }
-    // The attention workspace for every row count at full capacity (captured
-    // steps plan for max_seq_len), so no step ever needs to grow it.
+    // The attention workspace for every row count and every captured step's
+    // length bucket, so no step ever needs to grow it.
     size_t need = 0;
-    for (uint32_t b = 1; b <= c.max_batch; ++b) {
-        const size_t n = attention_ws_bytes(ctx, b, c.heads, c.kv_heads, c.head_dim, c.max_seq_len,
-                                            c.kv_dtype == JANUS_DT_F16);
-        need = n > need ? n : need;
-    }
+    for (uint32_t b = 1; b <= c.max_batch; ++b)
+        for (uint32_t k = 0; k < m->nbuckets; ++k) {
+            const size_t n = attention_ws_bytes(ctx, b, c.heads, c.kv_heads, c.head_dim, bucket_len(m, k),
+                                                c.kv_dtype == JANUS_DT_F16);
+            need = n > need ? n : need;
+        }
     if (need)
         if (int e = ensure_attn_ws(ctx, need)) {
             janus_model_destroy(m);
@@ -1083,7 +1145,8 @@ int janus_model_graph_begin_slots(janus_model *m, const uint32_t *tokens, const 
     if (int e = set_rows(m, in)) return e;
     JANUS_HIP_CHECK(ctx, hipMemsetAsync(m->d_counts, 0, (size_t)nseq * m->cfg.vocab * 4, ctx->stream));
     if (int e = upload_sampler(m)) return e;
-    if (int e = ensure_graph(m, nseq)) return e;
+    // every bucket from these rows' lengths up, so graph_run never captures
+    if (int e = replay_prepare(m, nseq, max_len, m->cfg.max_seq_len)) return e;
     m->h_pos.assign(positions, positions + nseq);
     m->graph_nseq = nseq;
     return JANUS_OK;
@@ -1096,11 +1159,14 @@ int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32
 int janus_model_graph_run(janus_model *m, uint32_t steps) {
     if (!m) return JANUS_E_INVALID_ARG;
     const uint32_t n = m->graph_nseq;
-    if (!n || !m->graphs[n]) return fail(m->ctx, JANUS_E_INVALID_ARG, "graph: call janus_model_graph_begin first");
-    for (uint32_t i = 0; i < n; ++i)
-        if (m->h_pos[i] + steps > m->cfg.max_seq_len)
+    if (!n) return fail(m->ctx, JANUS_E_INVALID_ARG, "graph: call janus_model_graph_begin first");
+    uint32_t top = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if ((uint64_t)m->h_pos[i] + steps > m->cfg.max_seq_len)
             return fail(m->ctx, JANUS_E_KV_OVERFLOW, "graph: steps would exceed max_seq_len");
-    if (int e = replay(m, n, steps)) return e;
+        top = m->h_pos[i] > top ? m->h_pos[i] : top;
+    }
+    if (int e = replay(m, n, steps, top + 1)) return e;
     for (auto &p : m->h_pos) p += steps;
     // a row whose step met NaN logits is stopped on the device; report it
     RowDev rows[kMaxRows];

@@ -356,6 +356,7 @@ int janus_create(int hip_device, janus_ctx **out) {
     if (const char *k = std::getenv("JANUS_GEMV_F16_ROWS")) ctx->gemv_f16_rows2 = std::strcmp(k, "1") != 0;
     if (const char *k = std::getenv("JANUS_GEMM_PIPE")) ctx->gemm_pipe = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_EPI_SPLIT")) ctx->epi_split = std::strcmp(k, "0") != 0;
+    if (const char *k = std::getenv("JANUS_GRAPH_BUCKETS")) ctx->graph_buckets = std::strcmp(k, "0") != 0;
     if (const char *k = std::getenv("JANUS_GEMM_KR")) {
         const long v = std::strtol(k, nullptr, 10);
         if (v == 256 || v == 512 || v == 1024) ctx->gemm_kr = (uint32_t)v;

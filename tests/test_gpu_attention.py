@@ -41,6 +41,28 @@ def test_attention_single_sequence(engine, kv, H, KVH, D, L):
     _close(out.cpu().numpy(), O.attention(q, k, v, H, KVH, D))
 
 
+@pytest.mark.parametrize("H,KVH,D", [(32, 8, 128), (32, 32, 128), (8, 1, 64)])
+@pytest.mark.parametrize("L,hint", [(65, 256), (300, 512), (700, 1024), (1500, 2048), (3000, 8192)])
+def test_attention_planned_for_a_longer_length(engine, H, KVH, D, L, hint):
+    """Captured decode steps plan attention for the length bucket above the
+    live context: the length read from the device, the plan made for
+    max_len_hint (one workgroup per head, per-query-head splits or KV-head
+    splits with a merge), fp16 cache, against the oracle."""
+    rng = np.random.default_rng(L + H + D)
+    q = rng.standard_normal(H * D).astype(np.float32)
+    k = rng.standard_normal((L, KVH, D)).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((L, KVH, D)).astype(np.float16).astype(np.float32)
+    kc = torch.zeros(hint, KVH, D, device=DEV, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    kc[:L] = torch.from_numpy(k).to(DEV, torch.float16)
+    vc[:L] = torch.from_numpy(v).to(DEV, torch.float16)
+    lens = torch.tensor([L], dtype=torch.int32, device=DEV)
+    out = torch.empty(H * D, device=DEV)
+    ops.compute_attention(engine, torch.from_numpy(q).to(DEV), kc, vc, out, 1, 0, hint, H, KVH, D, seq_lens=lens,
+                          max_len_hint=hint)
+    _close(out.cpu().numpy(), O.attention(q, k, v, H, KVH, D))
+
+
 def test_attention_zero_length_is_zero(engine):
     H, KVH, D = 4, 2, 64
     kc = torch.randn(8, KVH, D, device=DEV)

@@ -324,3 +324,66 @@ def test_nan_logits_refused_under_cpu_sampler_rules(engine):
     assert got == O.OracleModel(s, 32).generate(prompt, 6, 1.0)
     with pytest.raises(FloatingPointError):
         O.OracleModel(s, 32).generate(prompt, 2, 1.15)
+
+
+def _eager_tokens(m, prompt, steps, penalty):
+    """Eager steps after an eager prefill, sampled on the host from the GPU's
+    logits (penalty None: last-max argmax); returns the tokens and each
+    step's logits."""
+    for p, t in enumerate(prompt):
+        m.forward([t], [p])
+    last, pos, gen, logits = prompt[-1], len(prompt), [], []
+    for _ in range(steps):
+        m.forward([last], [pos])
+        lg = m.logits()[0]
+        logits.append(lg)
+        last = O.argmax_last(lg) if penalty is None else O.greedy_sample(lg, gen, penalty)
+        gen.append(last)
+        pos += 1
+    return gen, logits
+
+
+def test_captured_steps_cross_length_buckets(monkeypatch):
+    """Captured steps are planned per context-length bucket (256, 512, ...,
+    the last one max_seq_len): each replay runs the smallest bucket that
+    covers its longest row. With max_seq_len 600 the buckets are 256, 512
+    and 600. Graph decode from position 240 over two graph_run calls (the
+    second starting mid-bucket) crosses both edges; generate and
+    generate_with_callback cross 256 while prefilling and 512 while
+    decoding; generate_batch crosses them with its rows at different
+    positions. Each loop's tokens against eager steps sampled on the host
+    (identical, or parted only at a certified near tie), with the buckets and
+    with one step planned for max_seq_len (JANUS_GRAPH_BUCKETS=0)."""
+    s = synth.make_model(97, 512, 4, 1, 1024, 1000, 2, synth.Q4_0, 1e-5, 500000.0,
+                         embed_type=synth.F16, head_type=synth.F16)
+    prompt = _prompt(98, 240, s.vocab)
+    short = prompt[:100]
+    steps = 300   # positions 240..539
+    eng = ops.ComputeEngine(0)
+    m = Model(eng, s, max_seq_len=600, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+    want_arg, lg_arg = _eager_tokens(m, prompt, steps, None)
+    want_pen, lg_pen = _eager_tokens(m, prompt, steps, 1.15)
+    want_short, lg_short = _eager_tokens(m, short, steps, 1.15)
+    m.close()
+    eng.close()
+    for buckets in ("1", "0"):
+        monkeypatch.setenv("JANUS_GRAPH_BUCKETS", buckets)
+        eng = ops.ComputeEngine(0)
+        m = Model(eng, s, max_seq_len=600, max_batch=2, kv_dtype=_lib.DT_F16, act_dtype=_lib.DT_F16)
+        for p, t in enumerate(prompt):
+            m.forward([t], [p])
+        m.set_sampler(_lib.SAMPLER_ARGMAX)
+        m.graph_begin([prompt[-1]], [len(prompt)])
+        m.graph_run(100)
+        m.graph_run(steps - 100)
+        graph = m.generated(0)
+        gen = m.generate(prompt, steps, 1.15)
+        stream = m.generate_with_callback(prompt, steps, None, 1.15)
+        batch = m.generate_batch([prompt, short], steps, 1.15)
+        m.close()
+        eng.close()
+        assert len(graph) == len(gen) == len(stream) == steps and [len(b) for b in batch] == [steps, steps]
+        assert_same_or_near_tie(graph, want_arg, lg_arg, 1.0)
+        for got in (gen, stream, batch[0]):
+            assert_same_or_near_tie(got, want_pen, lg_pen, 1.15)
+        assert_same_or_near_tie(batch[1], want_short, lg_short, 1.15)
