@@ -80,7 +80,7 @@ int janus_model_read_logits(janus_model *m, float *h_out, uint32_t nseq);
  * tokens (:599-613) and the last-max argmax (:784-795). Stops at max_tokens,
  * at max_seq_len, or at 128001/128009 (generation.rs:241-260; the stop token
  * is not returned, as the reference does not push it). Runs on the device:
- * the decode step is captured once and replayed, the penalty's context is
+ * the decode step is captured (per context-length bucket) and replayed, the penalty's context is
  * kept as occurrence counts on the device and the sampled tokens are read
  * back in chunks. Sets the model's sampler (janus_model_set_sampler).
  * Under the penalty rule a NaN among a step's logits ends the call with
@@ -136,8 +136,13 @@ int janus_model_set_sampler(janus_model *m, int mode, float repetition_penalty);
  * ids, positions advanced on the device) for nseq sequences once, then replay
  * it `steps` times. janus_model_graph_begin sets sequence s to token
  * tokens[s] at position positions[s] in KV slot s (or slots[s]) and clears
- * its generated tokens. A captured step is kept per sequence count and
- * reused until a tensor or the KV cache is replaced. */
+ * its generated tokens. A step is captured per sequence count and per
+ * context-length bucket (256, 512, 1024, ... positions, the last one
+ * max_seq_len; its attention is planned for the bucket's length), and kept
+ * until a tensor or the KV cache is replaced; each replay runs the smallest
+ * bucket that covers its sequences. graph_begin captures every bucket from
+ * the sequences' current lengths up to max_seq_len, so graph_run never
+ * captures. */
 int janus_model_graph_begin(janus_model *m, const uint32_t *tokens, const uint32_t *positions, uint32_t nseq);
 int janus_model_graph_begin_slots(janus_model *m, const uint32_t *tokens, const uint32_t *positions,
                                   const uint32_t *slots, uint32_t nseq);
