@@ -5,9 +5,10 @@ Workload (headline metric "decode tok/s, Llama-3-8B-shape Q4_0, bs=1 &
   * value: batch-1 greedy decode tok/s of a random-init Llama-3-8B-architecture
     model (32 layers, hidden 4096, 32/8 heads, FFN 14336, vocab 128256, RoPE
     theta 5e5) with Q4_0 block weights, an F16 LM head, an fp16 KV cache and
-    fp16 activations into the products. A 128-token prompt is prefilled, then
-    each timed step is one HIP-graph decode step (embed -> 32 layers -> LM head
-    -> argmax fed back as the next token).
+    fp16 activations into the products, created at Llama-3-8B's 8192-token
+    context. A 128-token prompt is prefilled, then each timed step is one
+    HIP-graph decode step (embed -> 32 layers -> LM head -> argmax fed back as
+    the next token).
   * bs32: the ragged continuous-batch step of benchmark configuration 5 (32 sequences,
     fp16 KV contexts uniform in [256, 4096], one forward pass per step).
   * roofline: the dominant kernel, the Q4_0 GEMV at the 14336x4096 decode shape
@@ -566,7 +567,8 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (random-init weights, seeded prompt)",
         "config": {"workload": "Llama-3-8B-shape Q4_0 greedy decode, batch 1, 128-token prompt, fp16 KV, "
-                               "F16 LM head, HIP-graph decode step", "layers": args.layers,
+                               "F16 LM head, HIP-graph decode step, model at the 8192-token context",
+                   "layers": args.layers,
                    "hidden": 4096, "heads": 32, "kv_heads": 8, "ffn": 14336, "vocab": 128256},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": rec.get("traffic_bytes"),
