@@ -945,45 +945,73 @@ __global__ __launch_bounds__(D) void attn_merge_rows_kernel(AttnArgs a, uint32_t
 }
 
 // Merge: o = sum_s o_s e^{m_s - M} / sum_s l_s e^{m_s - M}, in one pass over
-// the splits with a running maximum; the partials of 8 splits are loaded
-// together, so a merge costs ns / 8 dependent round trips.
-template <int D>
+// the splits with a running maximum. The partials of the first SB planned
+// splits (8 or 16, the launch's choice) are requested together with the
+// sequence length, which decides how many of them are live (the others hold
+// earlier calls' values and are masked by selects), so a merge of up to SB
+// splits costs one dependent round trip; further splits follow SB at a time. The first batch is folded
+// whatever the length, so its loads stay ahead of the length's use; m and l
+// are read by lanes 0 and 1 (vector loads, issued with the o loads) and
+// broadcast.
+template <int D, uint32_t SB>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
-    constexpr int SB = 8;
     const uint32_t h = blockIdx.x, b = blockIdx.y;
+    const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);
+    const uint32_t len_raw = a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len;
+    float ml[SB], os[SB];
+    // splits s0 .. s0 + SB - 1 below lim; the rest re-read split s0 (in bounds)
+    auto load = [&](uint32_t s0, uint32_t lim) {
+#pragma unroll
+        for (uint32_t j = 0; j < SB; ++j) {
+            const float *ws = w + (size_t)(s0 + j < lim ? s0 + j : s0) * (D + 2);
+            ml[j] = ws[threadIdx.x & 1u];
+            os[j] = ws[2 + threadIdx.x];
+        }
+    };
+    load(0, a.splits);
+    __builtin_amdgcn_sched_barrier(0);   // the loads above issue before the length is waited for
     // lengths beyond the planned splits (or the capacity) are clamped, never read past
     const uint32_t span = a.nw * a.chunk;
-    const uint32_t len = min(min(a.seq_lens ? (uint32_t)a.seq_lens[b] : a.seq_len, a.max_seq), a.splits * span);
-    if (len <= span) return;   // written directly by the partial kernel
-    const uint32_t ns = (len + span - 1) / span;
-    const float *w = a.ws + ((size_t)b * a.heads + h) * a.splits * (D + 2);
+    const uint32_t len = min(min(len_raw, a.max_seq), a.splits * span);
+    // ns = 0: a single split, whose output the partial kernel wrote directly
+    const uint32_t nsr = (len + span - 1) / span;   // division first: no branch ahead of the loads' uses
+    const uint32_t ns = len > span ? nsr : 0;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (uint32_t s0 = 0; s0 < ns; s0 += SB) {
-        float ms[SB], ls[SB], os[SB];
+    for (uint32_t s0 = 0;;) {
+        float ms[SB];
 #pragma unroll
-        for (int j = 0; j < SB; ++j) {
-            const bool in = s0 + j < ns;
-            const float *ws = w + (size_t)(in ? s0 + j : s0) * (D + 2);
-            ms[j] = in ? ws[0] : -INFINITY;
-            ls[j] = in ? ws[1] : 0.0f;
-            os[j] = in ? ws[2 + threadIdx.x] : 0.0f;
+        for (uint32_t j = 0; j < SB; ++j) {
+            const bool live = s0 + j < ns;
+            ms[j] = live ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j]), 0)) : -INFINITY;
+            ml[j] = live ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml[j]), 1)) : 0.0f;
+            os[j] = live ? os[j] : 0.0f;
         }
         float Mn = M;
 #pragma unroll
-        for (int j = 0; j < SB; ++j) Mn = fmaxf(Mn, ms[j]);
-        if (Mn == -INFINITY) continue;   // no live split yet
-        const float r = fexp2(M - Mn);
-        L *= r;
-        o *= r;
+        for (uint32_t j = 0; j < SB; ++j) Mn = fmaxf(Mn, ms[j]);
+        if (Mn != -INFINITY) {   // else no live split yet
+            const float r = fexp2(M - Mn);
+            L *= r;
+            o *= r;
 #pragma unroll
-        for (int j = 0; j < SB; ++j) {
-            const float f = fexp2(ms[j] - Mn);   // 0 for the padding splits (m = -inf)
-            L = fmaf(ls[j], f, L);
-            o = fmaf(os[j], f, o);
+            for (uint32_t j = 0; j < SB; ++j) {
+                const float f = fexp2(ms[j] - Mn);   // 0 for masked splits (m = -inf)
+                L = fmaf(ml[j], f, L);
+                o = fmaf(os[j], f, o);
+            }
+            M = Mn;
         }
-        M = Mn;
+        s0 += SB;
+        if (s0 >= ns) break;
+        load(s0, ns);
     }
-    put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
+    if (ns) put_out(a, ((size_t)b * a.heads + h) * D + threadIdx.x, o / fmaxf(L, 1e-20f));
+}
+
+template <int D>
+void merge_launch(janus_ctx *ctx, const AttnArgs &a) {
+    if (a.splits <= 8) hipLaunchKernelGGL((attn_merge_kernel<D, 8>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+    else hipLaunchKernelGGL((attn_merge_kernel<D, 16>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
 }
 
 template <typename KV, int D>
@@ -996,7 +1024,7 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
         else hipLaunchKernelGGL((attn_decode_kernel<KV, D, 1, 16>), grid, block, lds, ctx->stream, a);
         JANUS_LAUNCH_CHECK(ctx);
         if (a.splits > 1) {
-            hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+            merge_launch<D>(ctx, a);
             JANUS_LAUNCH_CHECK(ctx);
         }
         return JANUS_OK;
@@ -1036,7 +1064,7 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
         }
         JANUS_LAUNCH_CHECK(ctx);
         if (a.splits > 1) {
-            hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+            merge_launch<D>(ctx, a);
             JANUS_LAUNCH_CHECK(ctx);
         }
         return JANUS_OK;
@@ -1060,7 +1088,7 @@ int launch_d(janus_ctx *ctx, const AttnArgs &a, uint32_t G) {
     }
     JANUS_LAUNCH_CHECK(ctx);
     if (a.splits > 1) {
-        hipLaunchKernelGGL((attn_merge_kernel<D>), dim3(a.heads, a.batch), dim3(D), 0, ctx->stream, a);
+        merge_launch<D>(ctx, a);
         JANUS_LAUNCH_CHECK(ctx);
     }
     return JANUS_OK;
