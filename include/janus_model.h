@@ -7,7 +7,8 @@
  * (:141-245), TransformerBlock::forward (model/block.rs:190-458) and the
  * generate loop (model/transformer/generation.rs:129-323). Each forward
  * enqueues the per-layer operator sequence on the context's stream; a decode
- * step can also be captured once into a HIP graph and replayed.
+ * step can also be captured into a HIP graph (per sequence count and
+ * context-length bucket) and replayed.
  */
 #ifndef JANUS_MODEL_H
 #define JANUS_MODEL_H

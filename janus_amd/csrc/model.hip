@@ -18,8 +18,9 @@
 // next step consumes, its position, the KV row base, the prompt still to
 // prefill, the generated tokens, their occurrence counts (the repetition
 // penalty's context) and a done flag. One step (forward, greedy choice,
-// advance) is either enqueued directly or captured once per row count into a
-// HIP graph and replayed; generate and generate_batch both run on replays.
+// advance) is either enqueued directly or captured per row count and
+// context-length bucket into a HIP graph and replayed; generate and
+// generate_batch both run on replays.
 #include <climits>
 #include <cmath>
 #include <cstdio>
