@@ -11,7 +11,11 @@
 - generate_batch (continuous batching, requests admitted into freed slots)
   gives every request the tokens it gets alone and the oracle's;
 - a workspace that grows after a capture does not invalidate the captured
-  step (the old buffer stays alive).
+  step (the old buffer stays alive);
+- captured steps per context-length bucket: graph_run, generate,
+  generate_with_callback and generate_batch across bucket edges give the
+  tokens of eager steps, with the buckets and with one step planned for
+  max_seq_len.
 """
 import numpy as np
 import pytest
