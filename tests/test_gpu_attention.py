@@ -63,6 +63,38 @@ def test_attention_planned_for_a_longer_length(engine, H, KVH, D, L, hint):
     _close(out.cpu().numpy(), O.attention(q, k, v, H, KVH, D))
 
 
+@pytest.mark.parametrize("kv", [torch.float32, torch.float16])
+@pytest.mark.parametrize("B", [2, 4, 8])
+@pytest.mark.parametrize("hint", [1024, 2048])
+def test_attention_small_batches_planned_lengths(engine, kv, B, hint):
+    """2, 4 and 8 sequences of 32 query / 8 KV heads, lengths up to the
+    plan's length (as in a captured step's bucket). Up to 1024 positions the
+    per-query-head launch: one workgroup per head when 4 or 8 sequences fill
+    half the CUs, splits with the merge kernel for 2. Beyond 1024 the KV-head
+    splits (f32 cache) or the task list (fp16 cache). Against the oracle."""
+    H, KVH, D = 32, 8, 128
+    rng = np.random.default_rng(B * 10 + hint)
+    lens = rng.integers(hint // 2 + 1, hint + 1, B).tolist()
+    lens[0] = hint
+    lens[-1] = hint // 2 + 1
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    total = int(sum(lens))
+    k = rng.standard_normal((total, KVH, D)).astype(np.float32)
+    v = rng.standard_normal((total, KVH, D)).astype(np.float32)
+    if kv == torch.float16:
+        k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+    q = rng.standard_normal((B, H * D)).astype(np.float32)
+    out = torch.full((B, H * D), 7.0, device=DEV)
+    ops.compute_attention(engine, torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV, kv),
+                          torch.from_numpy(v).to(DEV, kv), out, B, 0, hint, H, KVH, D,
+                          row_base=torch.from_numpy(offs).to(DEV),
+                          seq_lens=torch.tensor(lens, dtype=torch.int32, device=DEV), max_len_hint=hint)
+    got = out.cpu().numpy()
+    for b in range(B):
+        sl = slice(offs[b], offs[b] + lens[b])
+        _close(got[b], O.attention(q[b], k[sl], v[sl], H, KVH, D))
+
+
 def test_attention_zero_length_is_zero(engine):
     H, KVH, D = 4, 2, 64
     kc = torch.randn(8, KVH, D, device=DEV)
