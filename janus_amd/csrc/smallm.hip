@@ -549,7 +549,7 @@ __global__ __launch_bounds__(64 * WAVES * KW) void gemm_mfma_kernel(GemmArgs a) 
 }
 
 // Sums the split-K partials in split order and applies the epilogue.
-// Cross-pass pipelined form of gemm_mfma_kernel for the quantised formats,
+// Cross-pass pipelined form of gemm_mfma_kernel (quantised and F16 weights),
 // with the pass length KR fixed at compile time. A is double-buffered in LDS:
 // the activations of pass p + 1 are requested while pass p computes and are
 // stored at its end; each wavefront keeps one pass of weight chunks in
@@ -973,8 +973,10 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     if (tiles * ((w->t32_chunks * F::CK + kr - 1) / kr) < want && kr / F::CK >= 2 * KW) kr /= 2;
     uint32_t ks = 0;
     bool pipe = false;
-    if constexpr (!std::is_same<F, GF16>::value) {
-        // pipelined kernel (quantised weights): 256-long passes, K split until
+    {
+        // pipelined kernel (F16 LM head 128256x4096 at M = 32: 181.5 us
+        // against 209.3 single-buffered; 512- / 1024-long passes 182.8 /
+        // 188.4 us): 256-long passes, K split until
         // about 1.1 workgroups per CU, used when every workgroup then runs at
         // least 3 passes (fewer leave nothing to overlap)
         if (ctx->gemm_pipe && !kr_force && !ks_force) {
@@ -1028,9 +1030,9 @@ int launch_mfma(janus_ctx *ctx, GemmArgs a, const janus_weight *w, GemmPartials 
     }();
     (void)attr_set;
     const dim3 grid(tiles, a.ksplit), block(64 * WAVES * KW);
-    // quantised weights: the cross-pass pipelined kernel for the usual pass lengths
+    // the cross-pass pipelined kernel for the usual pass lengths
     bool piped = false;
-    if constexpr (!std::is_same<F, GF16>::value) {
+    {
         if (pipe && a.passes_per_wg > 1) {
             piped = true;
             if (kr == 256) launch_pipe<F, MT, KW, 256>(ctx, grid, a);
